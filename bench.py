@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Fused-MoE benchmark on one MI355X.
+
+A step is one full fused-MoE forward (route -> align -> Stage 1 -> Stage 2 ->
+combine) over one batch of synthetic, seeded inputs already resident in HBM.
+Default workload: BASELINE.json's headline config (DeepSeek-V3-style prefill,
+T=4096 H=7168 I=2048 E=256 top-8, fp16, expert bias ~N(0, 0.5)).
+
+Prints ONE JSON line (see the keys at the end of main()).  Per-kernel times
+come from HIP events recorded on the launch stream between the stages
+(moe_fused_forward_events); the CPU baseline is the oracle's fp32 expert loop
+on a bounded sample of experts, timed on this host.
+
+    python bench.py [--steps K] [--warmup W] [--config dsv3] [--no-cpu] [--no-check]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+CONFIGS = {  # name -> (T, H, I, E, k, bias kind)
+    "small": (128, 1024, 512, 8, 2, None),
+    "mixtral": (2048, 4096, 14336, 8, 2, None),
+    "dsv3": (4096, 7168, 2048, 256, 8, "normal"),
+    "decode": (32, 7168, 2048, 256, 8, "zipf"),
+    "w8a8": (2048, 7168, 2048, 64, 6, None),
+}
+METRIC = "fused-MoE ms & TFLOP/s (%MFMA peak), H7168 I2048 E256 top8 T4096 fp16"
+PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0
+PEAK_I8_TOPS = 5000.0
+SEED = 20261201
+
+
+def make_inputs(name, dev):
+    import torch
+    T, H, I, E, k, bias_kind = CONFIGS[name]
+    g = torch.Generator(device="cpu").manual_seed(SEED)
+    x = torch.randn((T, H), generator=g, dtype=torch.float16).to(dev)
+    logits = torch.randn((T, E), generator=g).to(dev)
+    bias = None
+    if bias_kind == "normal":
+        bias = (torch.randn((E,), generator=g) * 0.5).to(dev)
+    elif bias_kind == "zipf":
+        bias = (-1.2 * torch.log(torch.arange(E, dtype=torch.float32) + 1)).to(dev)
+    gd = torch.Generator(device=dev).manual_seed(SEED + 1)
+    wg = torch.randn((E, I, H), generator=gd, device=dev, dtype=torch.float16) * 0.02
+    wu = torch.randn((E, I, H), generator=gd, device=dev, dtype=torch.float16) * 0.02
+    wd = torch.randn((E, H, I), generator=gd, device=dev, dtype=torch.float16) * 0.02
+    return dict(x=x, logits=logits, bias=bias, wg=wg, wu=wu, wd=wd, T=T, H=H, I=I, E=E, k=k)
+
+
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime torch already loaded."""
+
+    def __init__(self, n):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.ev = (ctypes.c_void_p * n)()
+        for i in range(n):
+            rc = self.hip.hipEventCreate(ctypes.byref(self.ev, i * ctypes.sizeof(ctypes.c_void_p)))
+            if rc:
+                raise RuntimeError(f"hipEventCreate failed: {rc}")
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(self.ev[a]),
+                                          ctypes.c_void_p(self.ev[b]))
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(ctypes.c_void_p(e))
+
+
+def cpu_baseline(inp, ids_np, budget_s=15.0):
+    """The oracle's fp32 expert loop (problem_detail.json:50 restated) on a
+    bounded sample of experts of this routing, timed on the host; returns
+    TFLOP/s of routed expert FLOPs."""
+    import numpy as np
+    import torch
+    from oracle import align, gather_rows, prerouted_forward
+    T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
+    torch.set_num_threads(os.cpu_count() or 1)
+    al = align(ids_np, E, 128)
+    xs = gather_rows(inp["x"].cpu(), al["sorted_pair_ids"], k)
+    gs = al["group_sizes"]
+    order = [e for e in range(E) if gs[e] > 0]
+    routed = torch.ones(int(al["group_offsets"][-1]))
+    done_rows, spent, used = 0, 0.0, []
+    wcpu = {}
+    for e in order:  # grow the sample until the time budget is used
+        wcpu_e = (inp["wg"][e].cpu(), inp["wu"][e].cpu(), inp["wd"][e].cpu())
+        wg = {e: wcpu_e[0]}
+        wu = {e: wcpu_e[1]}
+        wd = {e: wcpu_e[2]}
+        t0 = time.perf_counter()
+        prerouted_forward(xs, wg, wu, wd, routed, gs, al["group_offsets"], al["group_padded_offsets"],
+                          experts=[e])
+        spent += time.perf_counter() - t0
+        done_rows += int(gs[e])
+        used.append(e)
+        if spent >= budget_s:
+            break
+    flops = 6.0 * H * I * done_rows
+    return dict(value=round(flops / spent / 1e12, 4), unit="TFLOP/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=(f"oracle fp32 per-expert loop (torch CPU) over {len(used)} of {len(order)} "
+                        f"routed experts = {done_rows} of {T * k} routed rows, {spent:.1f} s; "
+                        f"routing/align/combine excluded; host {platform.processor() or 'x86_64'}, "
+                        f"os.cpu_count()={os.cpu_count()}"))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="dsv3", choices=list(CONFIGS))
+    ap.add_argument("--block-m", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-check", action="store_true", help="skip the sampled oracle check")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import muxi_race_amd as m
+    from muxi_race_amd._lib import check, lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = make_inputs(args.config, dev)
+    T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
+    L = lib()
+    bm = args.block_m or int(L.moe_pick_block_m(T, E, k))
+    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, k), dtype=torch.float32, device=dev)
+    P = ctypes.c_void_p
+    stream = P(torch.cuda.current_stream(dev).cuda_stream)
+    cargs = [P(inp["x"].data_ptr()), P(inp["logits"].data_ptr()),
+             P(0 if inp["bias"] is None else inp["bias"].data_ptr()), P(inp["wg"].data_ptr()),
+             P(inp["wu"].data_ptr()), P(inp["wd"].data_ptr()), P(out.data_ptr()), T, H, I, E, k, bm,
+             P(ws.data_ptr()), ws.numel(), P(ids.data_ptr()), P(wts.data_ptr()), stream]
+
+    def step(events=None):
+        if events is None:
+            check(L.moe_fused_forward(*cargs), "moe_fused_forward")
+        else:
+            check(L.moe_fused_forward_events(*cargs, events), "moe_fused_forward_events")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # headline: K steps bracketed by synchronisation, per-step events for the median
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    evs[0].record()
+    for i in range(args.steps):
+        step()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+
+    # per-stage durations on the launch stream
+    stage_names = ["route", "align", "quant_x", "stage1", "stage2", "combine"]
+    hev = HipEvents(7 * args.steps)
+    for i in range(args.steps):
+        step(ctypes.cast(ctypes.byref(hev.ev, 7 * i * ctypes.sizeof(ctypes.c_void_p)),
+                         ctypes.POINTER(ctypes.c_void_p)))
+    torch.cuda.synchronize()
+    stage = {n: [] for n in stage_names}
+    for i in range(args.steps):
+        for j, n in enumerate(stage_names):
+            stage[n].append(hev.elapsed_ms(7 * i + j, 7 * i + j + 1))
+    hev.close()
+    stage_ms = {n: round(statistics.mean(v), 4) for n, v in stage.items()}
+
+    # algorithmic work
+    ids_np = ids.cpu().numpy()
+    touched = np.unique(ids_np).size
+    Pn = T * k
+    flops = 6.0 * H * I * Pn
+    op_bytes = touched * 3.0 * H * I * 2 + 2.0 * T * H * 2 + T * E * 4 + Pn * 8
+    s1_bytes = touched * 2.0 * H * I * 2 + T * H * 2 + Pn * I * 2
+    s1_flops = 4.0 * H * I * Pn
+    s1_ms = stage_ms["stage1"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = op_bytes / (ms * 1e-3) / 1e9
+    ideal_ms = max(flops / (PEAK_F16_TFLOPS * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
+
+    check_res = None
+    if not args.no_check:
+        from oracle import fused_moe_forward, route_topk
+        rid, _ = route_topk(inp["logits"].cpu().numpy(), k,
+                            None if inp["bias"] is None else inp["bias"].cpu().numpy())
+        ids_ok = bool(np.array_equal(ids_np, rid))
+        rows = np.sort(np.random.default_rng(0).choice(T, min(T, 4), replace=False))
+        r = torch.from_numpy(rows).to(dev)
+        ref = fused_moe_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), inp["wg"], inp["wu"],
+                                inp["wd"], k, None if inp["bias"] is None else inp["bias"].cpu()).float()
+        got = out[r].float().cpu()
+        ok = bool(torch.isfinite(got).all()) and bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
+        check_res = dict(routing_ids_bit_exact=ids_ok, sampled_tokens=len(rows),
+                         within_rtol2e-2_atol1e-2=ok)
+
+    cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
+
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "ms_per_step_median": round(statistics.median(per), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded: x~N(0,1), weights~N(0,0.02), logits~N(0,1)"
+                + (", bias~N(0,0.5)" if CONFIGS[args.config][5] == "normal" else "")
+                + (", bias=-1.2*ln(rank+1)" if CONFIGS[args.config][5] == "zipf" else "") + ")",
+        "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} fp16",
+                   "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
+                   "block_m": bm, "experts_touched": int(touched)},
+        "gb_per_s": round(gbs, 1),
+        "frac_mfma_peak": round(tflops / PEAK_F16_TFLOPS, 4),
+        "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+        "roofline_ideal_ms": round(ideal_ms, 4),
+        "frac_of_roofline_time": round(ideal_ms / ms, 4),
+        "stage_ms": stage_ms,
+        "roofline": {
+            "kernel": "stage1 (gathered gate/up GEMM + SiLU*up)",
+            "bound": "hbm",
+            "achieved": round(s1_bytes / (s1_ms * 1e-3) / 1e9, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(s1_bytes / (s1_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": int(s1_bytes),
+            "mfma_tflops": round(s1_flops / (s1_ms * 1e-3) / 1e12, 2),
+        },
+        "cpu_baseline": cpu,
+        "check": check_res,
+        "wall_ms_timed_region": round(wall_ms, 2),
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

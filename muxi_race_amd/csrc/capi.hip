@@ -1,0 +1,299 @@
+// extern "C" entry points of libmoe_gfx950.so (declared in include/moe_gfx950.h).
+// Host-side only: argument validation, workspace carving, launch order.  All
+// work is enqueued on the caller's stream; nothing here allocates or waits.
+#include "../../include/moe_gfx950.h"
+#include "launch.h"
+#include "moe_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MOE_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return MOE_OK;
+}
+
+constexpr int64_t kAlign = 256;
+int64_t up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+int64_t cap_rows(int64_t T, int64_t k, int64_t E, int64_t bm) {
+  const int64_t P = T * k;
+  const int64_t owners = E < P ? E : P;
+  return (P + owners * (bm - 1)) / bm * bm;
+}
+
+struct FusedLayout {
+  int64_t ids, w, sorted, bexp, gs, go, gpo, h, hs, xq, sx, ypair, total;
+};
+
+FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm,
+                         bool w8) {
+  FusedLayout L{};
+  const int64_t P = T * k, rows = cap_rows(T, k, E, bm);
+  int64_t o = 0;
+  L.ids = o; o += up(P * 4);
+  L.w = o; o += up(P * 4);
+  L.sorted = o; o += up(rows * 4);
+  L.bexp = o; o += up((rows / bm) * 4);
+  L.gs = o; o += up(E * 4);
+  L.go = o; o += up((E + 1) * 4);
+  L.gpo = o; o += up((E + 1) * 4);
+  L.h = o; o += up(rows * I * (w8 ? 1 : 2));
+  L.hs = o; o += w8 ? up(rows * (I / moe::kBN) * 4) : 0;
+  L.xq = o; o += w8 ? up(T * H) : 0;
+  L.sx = o; o += w8 ? up(T * 4) : 0;
+  L.ypair = o; o += up(P * H * 2);
+  L.total = o;
+  return L;
+}
+
+int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
+  const int64_t avg = E > 0 ? (T * k + E - 1) / E : 0;
+  if (avg <= 32) return 32;
+  if (avg <= 64) return 64;
+  return 128;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_dims(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm) {
+  if (T < 0 || E <= 0 || k <= 0) return fail(MOE_ERR_INVALID_ARG, "bad sizes T=%lld E=%lld k=%lld", (long long)T, (long long)E, (long long)k);
+  if (k > E || k > 32) return fail(MOE_ERR_UNSUPPORTED, "top_k=%lld must be <= min(E, 32)", (long long)k);
+  if (E > 1024) return fail(MOE_ERR_UNSUPPORTED, "E=%lld > 1024", (long long)E);
+  if (H <= 0 || I <= 0 || H % 128 || I % 128) return fail(MOE_ERR_UNSUPPORTED, "H=%lld and I=%lld must be positive multiples of 128", (long long)H, (long long)I);
+  if (bm != 32 && bm != 64 && bm != 128) return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {32,64,128}", (long long)bm);
+  if (cap_rows(T, k, E, bm) * I >= ((int64_t)1 << 31) * 2 || T * k >= ((int64_t)1 << 31)) return fail(MOE_ERR_UNSUPPORTED, "problem too large for 32-bit row indices");
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_version(void) { return 1; }
+
+const char* moe_last_error_string(void) { return g_err; }
+
+int64_t moe_prerouted_workspace_bytes(int64_t P, int64_t I) { return P > 0 && I > 0 ? P * I * 2 : 0; }
+
+int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const void* w_down,
+                      const void* routed, int routed_dtype, const int32_t* group_sizes,
+                      const int32_t* group_offsets, const int32_t* group_padded_offsets,
+                      const int32_t* group_idx_for_bx, void* out, int64_t P, int64_t H, int64_t I,
+                      int64_t E, int64_t V, int64_t nblk, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  (void)group_idx_for_bx;  // block -> expert follows from group_padded_offsets
+  if (P < 0 || H <= 0 || I <= 0 || E <= 0 || V < 0 || nblk < 0)
+    return fail(MOE_ERR_INVALID_ARG, "bad sizes P=%lld H=%lld I=%lld E=%lld V=%lld", (long long)P, (long long)H, (long long)I, (long long)E, (long long)V);
+  if (P == 0) return MOE_OK;  // nothing to write (submission.py:2117-2120)
+  if (H % 128 || I % 128 || P % 128)
+    return fail(MOE_ERR_UNSUPPORTED, "H=%lld, I=%lld and P=%lld must be multiples of 128", (long long)H, (long long)I, (long long)P);
+  if (E > 65536) return fail(MOE_ERR_UNSUPPORTED, "E=%lld too large", (long long)E);
+  if (P * (H > I ? H : I) >= ((int64_t)1 << 40)) return fail(MOE_ERR_UNSUPPORTED, "problem too large");
+  if (routed_dtype != MOE_ROUTED_F32 && routed_dtype != MOE_ROUTED_F16)
+    return fail(MOE_ERR_INVALID_ARG, "routed_dtype=%d", routed_dtype);
+  if (!x || !w_gate || !w_up || !w_down || !group_sizes || !group_offsets || !group_padded_offsets || !out || (V > 0 && !routed))
+    return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) || !aligned16(out) || !aligned16(workspace))
+    return fail(MOE_ERR_INVALID_ARG, "x, weights, out and workspace must be 16-byte aligned");
+  if (workspace_bytes < moe_prerouted_workspace_bytes(P, I) || !workspace)
+    return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)moe_prerouted_workspace_bytes(P, I));
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t blocks = P / 128;  // x, out and the workspace hold P rows
+
+  moe::Stage1Params p1{};
+  p1.x = (const char*)x;
+  p1.wg = (const char*)w_gate;
+  p1.wu = (const char*)w_up;
+  p1.h = (char*)workspace;
+  p1.gs = group_sizes;
+  p1.gpo = group_padded_offsets;
+  p1.topk = 1;
+  p1.E = (int)E;
+  p1.H = H;
+  p1.I = I;
+  int rc = check_launch(moe::launch_stage1(p1, 128, false, false, blocks, s), "stage1");
+  if (rc) return rc;
+
+  moe::Stage2Params p2{};
+  p2.a = (const char*)workspace;
+  p2.wd = (const char*)w_down;
+  p2.out = (char*)out;
+  p2.routed = routed;
+  p2.routed_f16 = routed_dtype == MOE_ROUTED_F16;
+  p2.gs = group_sizes;
+  p2.go = group_offsets;
+  p2.gpo = group_padded_offsets;
+  p2.E = (int)E;
+  p2.H = H;
+  p2.I = I;
+  p2.V = V;
+  return check_launch(moe::launch_stage2(p2, 128, false, false, blocks, s), "stage2");
+}
+
+int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k,
+                   int32_t* topk_ids, float* topk_weights, void* stream) {
+  if (T < 0 || E <= 0 || k <= 0) return fail(MOE_ERR_INVALID_ARG, "bad sizes T=%lld E=%lld k=%lld", (long long)T, (long long)E, (long long)k);
+  if (E > 1024 || k > 32 || k > E) return fail(MOE_ERR_UNSUPPORTED, "need E <= 1024 and k <= min(E, 32)");
+  if (T == 0) return MOE_OK;
+  if (!logits || !topk_ids || !topk_weights) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, topk_ids, topk_weights, (hipStream_t)stream), "route_topk");
+}
+
+int64_t moe_align_capacity_rows(int64_t T, int64_t k, int64_t E, int64_t block_m) {
+  if (T < 0 || k <= 0 || E <= 0 || block_m <= 0) return 0;
+  return cap_rows(T, k, E, block_m);
+}
+
+int moe_align(const int32_t* topk_ids, int64_t T, int64_t k, int64_t E, int64_t block_m,
+              int32_t* sorted_pair_ids, int32_t* block_expert, int32_t* group_sizes,
+              int32_t* group_offsets, int32_t* group_padded_offsets, void* stream) {
+  if (T < 0 || k <= 0 || E <= 0 || block_m <= 0) return fail(MOE_ERR_INVALID_ARG, "bad sizes");
+  if (E > 1024) return fail(MOE_ERR_UNSUPPORTED, "E=%lld > 1024", (long long)E);
+  if (T * k >= ((int64_t)1 << 30)) return fail(MOE_ERR_UNSUPPORTED, "too many pairs");
+  if ((T > 0 && (!topk_ids || !sorted_pair_ids || !block_expert)) || !group_sizes || !group_offsets || !group_padded_offsets)
+    return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return check_launch(moe::launch_align(topk_ids, (int)(T * k), (int)E, (int)block_m, sorted_pair_ids, block_expert, group_sizes, group_offsets, group_padded_offsets, (hipStream_t)stream), "align");
+}
+
+int64_t moe_pick_block_m(int64_t T, int64_t E, int64_t k) { return pick_bm(T, E, k); }
+
+int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                  int64_t block_m, int w8a8) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  if (block_m == 0) block_m = pick_bm(T, E, k);
+  return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
+}
+
+static int fused_common(bool w8, const void* x, const float* logits, const float* bias,
+                        const void* wg, const float* sg, const void* wu, const float* su,
+                        const void* wd, const float* sd, void* out, int64_t T, int64_t H,
+                        int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
+                        int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
+                        void* const* ev) {
+  if (block_m == 0) block_m = pick_bm(T, E, k);
+  int rc = check_dims(T, H, I, E, k, block_m);
+  if (rc) return rc;
+  if (T == 0) return MOE_OK;
+  if (!x || !logits || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
+    return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))))
+    return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
+  const FusedLayout L = fused_layout(T, H, I, E, k, block_m, w8);
+  if (workspace_bytes < L.total) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);
+  float* wts = w_out ? w_out : (float*)(ws + L.w);
+  int32_t* sorted = (int32_t*)(ws + L.sorted);
+  int32_t* gs = (int32_t*)(ws + L.gs);
+  int32_t* go = (int32_t*)(ws + L.go);
+  int32_t* gpo = (int32_t*)(ws + L.gpo);
+  const int64_t rows = cap_rows(T, k, E, block_m);
+
+  // optional stage markers: ev[0] start, [1] routed, [2] aligned, [3] x quantised,
+  // [4] stage 1, [5] stage 2, [6] combined
+  auto mark = [&](int i) { if (ev && ev[i]) (void)hipEventRecord((hipEvent_t)ev[i], s); };
+  mark(0);
+  if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s), "route_topk"))) return rc;
+  mark(1);
+  if ((rc = check_launch(moe::launch_align(ids, (int)(T * k), (int)E, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, s), "align"))) return rc;
+  mark(2);
+  if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, (int8_t*)(ws + L.xq), (float*)(ws + L.sx), s), "quantize_x"))) return rc;
+  mark(3);
+
+  moe::Stage1Params p1{};
+  p1.x = w8 ? (const char*)(ws + L.xq) : (const char*)x;
+  p1.wg = (const char*)wg;
+  p1.wu = (const char*)wu;
+  p1.h = ws + L.h;
+  p1.h_scale = w8 ? (float*)(ws + L.hs) : nullptr;
+  p1.x_scale = w8 ? (const float*)(ws + L.sx) : nullptr;
+  p1.sg = sg;
+  p1.su = su;
+  p1.gs = gs;
+  p1.gpo = gpo;
+  p1.sorted_ids = sorted;
+  p1.topk = (int)k;
+  p1.E = (int)E;
+  p1.H = H;
+  p1.I = I;
+  if ((rc = check_launch(moe::launch_stage1(p1, (int)block_m, w8, true, rows / block_m, s), "stage1"))) return rc;
+  mark(4);
+
+  moe::Stage2Params p2{};
+  p2.a = ws + L.h;
+  p2.a_scale = w8 ? (const float*)(ws + L.hs) : nullptr;
+  p2.wd = (const char*)wd;
+  p2.sd = sd;
+  p2.out = ws + L.ypair;
+  p2.routed = wts;
+  p2.routed_f16 = 0;
+  p2.gs = gs;
+  p2.go = go;
+  p2.gpo = gpo;
+  p2.sorted_ids = sorted;
+  p2.E = (int)E;
+  p2.H = H;
+  p2.I = I;
+  if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, w8, true, rows / block_m, s), "stage2"))) return rc;
+  mark(5);
+  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)k, out, s), "combine");
+  mark(6);
+  return rc;
+}
+
+int moe_fused_forward(const void* x, const float* logits, const float* bias, const void* w_gate,
+                      const void* w_up, const void* w_down, void* out, int64_t T, int64_t H,
+                      int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
+                      int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
+                      void* stream) {
+  return fused_common(false, x, logits, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+                      T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
+                      topk_weights_out, stream, nullptr);
+}
+
+int moe_fused_forward_events(const void* x, const float* logits, const float* bias,
+                             const void* w_gate, const void* w_up, const void* w_down, void* out,
+                             int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                             int64_t block_m, void* workspace, int64_t workspace_bytes,
+                             int32_t* topk_ids_out, float* topk_weights_out, void* stream,
+                             void* const* stage_events) {
+  return fused_common(false, x, logits, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+                      T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
+                      topk_weights_out, stream, stage_events);
+}
+
+int moe_quantize_rows_w8(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+                         void* stream) {
+  if (R < 0 || K <= 0 || K % 8) return fail(MOE_ERR_INVALID_ARG, "need R >= 0 and K a positive multiple of 8");
+  if (R == 0) return MOE_OK;
+  if (!w || !q || !scale) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (!aligned16(w) || ((uintptr_t)q & 7)) return fail(MOE_ERR_INVALID_ARG, "w must be 16-byte and q 8-byte aligned");
+  return check_launch(moe::launch_quant_rows(w, R, K, q, scale, (hipStream_t)stream), "quantize_rows");
+}
+
+int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias,
+                           const int8_t* wq_gate, const float* s_gate, const int8_t* wq_up,
+                           const float* s_up, const int8_t* wq_down, const float* s_down,
+                           void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                           int64_t block_m, void* workspace, int64_t workspace_bytes,
+                           int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
+  return fused_common(true, x, logits, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+                      T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
+                      topk_weights_out, stream, nullptr);
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// Internal launcher interface between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Stage 1: h = silu(X Wg^T) * (X Wu^T) for the rows of every M block.
+struct Stage1Params {
+  const char* x;            // fp16 [rows, H] (direct) / fp16|int8 [T, H] (gather)
+  const char* wg;           // [E, I, H]
+  const char* wu;           // [E, I, H]
+  char* h;                  // fp16|int8 [padded rows, I]
+  float* h_scale;           // int8 only: [padded rows, I/128]
+  const float* x_scale;     // int8 only: [T]
+  const float* sg;          // int8 only: [E, I]
+  const float* su;          // int8 only: [E, I]
+  const int32_t* gs;        // [E]
+  const int32_t* gpo;       // [E+1]
+  const int32_t* sorted_ids;  // gather only: [padded rows], sentinel = T*topk
+  int topk;
+  int E;
+  int64_t H;
+  int64_t I;
+  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher)
+};
+
+// Stage 2: y = h Wd^T, scaled by the routing weight of each row.
+struct Stage2Params {
+  const char* a;            // fp16|int8 [padded rows, I]
+  const float* a_scale;     // int8 only: [padded rows, I/128]
+  const char* wd;           // [E, H, I]
+  const float* sd;          // int8 only: [E, H]
+  char* out;                // pre-routed: fp16 [P, H]; fused: fp16 [T*topk, H]
+  const void* routed;       // pre-routed: [V] raw order (fp32|fp16); fused: fp32 [T*topk]
+  int routed_f16;
+  const int32_t* gs;
+  const int32_t* go;
+  const int32_t* gpo;
+  const int32_t* sorted_ids;  // fused only
+  int E;
+  int64_t H;
+  int64_t I;
+  int64_t V;                // pre-routed: entries of `routed` (raw index is clamped to V-1)
+  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher)
+};
+
+hipError_t launch_stage1(const Stage1Params& p, int block_m, bool int8, bool gather,
+                         int64_t max_blocks, hipStream_t stream);
+hipError_t launch_stage2(const Stage2Params& p, int block_m, bool int8, bool fused,
+                         int64_t max_blocks, hipStream_t stream);
+
+hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
+                             int32_t* ids, float* w, hipStream_t stream);
+hipError_t launch_align(const int32_t* ids, int P, int E, int block_m, int32_t* sorted_ids,
+                        int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
+                        hipStream_t stream);
+hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
+                          hipStream_t stream);
+hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+                             hipStream_t stream);
+
+}  // namespace moe

@@ -1,0 +1,178 @@
+// Shared device-side building blocks for the gfx950 fused-MoE kernels.
+//
+// Tile geometry.  Every GEMM operand tile is a stack of rows that are
+// contiguous along K in global memory (token rows of x / the intermediate,
+// output-feature rows of the expert weights).  One K step moves 128 bytes of
+// each row (64 fp16 or 128 int8 elements) = eight 16-byte chunks.  In LDS a
+// row occupies 128 bytes and chunk c of row r sits at chunk slot
+// c ^ swz(r), so the 32 rows read by one MFMA fragment load spread over the
+// banks.  One MFMA K sub-step consumes two chunks per row (lanes 0-31 the
+// first, lanes 32-63 the second), i.e. 16 fp16 or 32 int8 per row.
+//
+// MFMA roles.  D[n][m] = sum_k W[n][k] * X[m][k]: the weight tile is the A
+// operand (32 output features per MFMA block) and the token tile the B
+// operand (32 tokens).  In the 32x32 accumulator lane l holds token
+// m = l % 32 and features n = 8*(r/4) + 4*(l/32) + r%4 for register r, so each
+// lane owns runs of 4 consecutive output features of one token row: the
+// epilogues store 8-byte (fp16) or 4-byte (int8) vectors.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;      // 4 waves per workgroup
+constexpr int kRowBytes = 128;     // bytes of one tile row per K step
+constexpr int kBN = 128;           // output-feature tile (N) of every GEMM
+constexpr int kNumXcd = 8;         // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr float kLog2e = 1.44269504088896341f;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// LDS byte offset of 16-byte chunk c of tile row r.
+__device__ __forceinline__ int lds_swz(int r, int c) {
+  return (r << 7) | (((c ^ r) & 7) << 4);
+}
+
+// Global -> register -> LDS loader for a tile of ROWS rows x 128 bytes.
+// Thread t moves chunks (row = t/8 + 32*i, chunk = t%8): eight consecutive
+// lanes cover one 128-byte row segment, so every wave load is 8 fully used
+// 128-byte lines.
+template <int ROWS>
+struct TileLoader {
+  static constexpr int CH = ROWS * 8 / kThreads;
+  static_assert(CH >= 1 && ROWS * 8 == CH * kThreads, "tile rows must be a multiple of 32");
+  const char* src[CH];
+  int dst[CH];
+  u32x4 reg[CH];
+
+  __device__ __forceinline__ static int row_of(int i) { return (threadIdx.x >> 3) + 32 * i; }
+
+  // rowp: address of K-step 0 of tile row row_of(i).
+  __device__ __forceinline__ void set(int i, const char* rowp) {
+    const int c = threadIdx.x & 7;
+    src[i] = rowp + (c << 4);
+    dst[i] = lds_swz(row_of(i), c);
+  }
+  __device__ __forceinline__ void load(int ks) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + (size_t)ks * kRowBytes);
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(lds + dst[i]) = reg[i];
+  }
+};
+
+// MFMA fragment of the 32 tile rows starting at `row0`, K sub-step s (0..3).
+__device__ __forceinline__ u32x4 frag(const char* lds, int row0, int s) {
+  const int l = lane_id();
+  return *reinterpret_cast<const u32x4*>(lds + lds_swz(row0 + (l & 31), 2 * s + (l >> 5)));
+}
+
+__device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x16 mma(u32x4 a, u32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a),
+                                              __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// silu(g) * u = u * g / (1 + 2^(-g*log2e)) in fp32 (v_exp_f32 + v_rcp_f32).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
+  return u * (g * sig);
+}
+
+// q = clamp(trunc(x*inv +- 0.5), +-127): the product and the +-0.5 are two
+// separately rounded fp32 operations (never one fused multiply-add), so the
+// result is bit-identical to the same two IEEE operations on the CPU.
+__device__ __forceinline__ int quant_i8(float x, float inv) {
+#pragma clang fp contract(off)
+  const float v = x * inv;
+  float t = v + (v >= 0.0f ? 0.5f : -0.5f);
+  int q = (int)t;  // truncates toward zero
+  q = q > 127 ? 127 : q;
+  q = q < -127 ? -127 : q;
+  return q;
+}
+
+// ---------------------------------------------------------------------------
+// Work schedule.  A launch covers items (expert e, N tile n, M block m) of all
+// experts.  Items are numbered expert-major, then N tile, then M block, so the
+// M blocks of one expert that share a weight tile are adjacent; the item range
+// is cut into 8 contiguous chunks, one per XCD (workgroup g runs on XCD g % 8
+// and is that XCD's (g / 8)-th workgroup), so an expert's weight tiles and
+// token tiles are re-read from that XCD's L2 rather than from HBM.
+// M blocks of expert e are [gpo[e]/BM, gpo[e+1]/BM).  `host_blocks` is the
+// number of BM-row blocks the caller's buffers hold: expert blocks beyond it
+// are never scheduled (so inconsistent metadata cannot move an access out of
+// the buffers), and with `tail` set, blocks between the experts' last block
+// and host_blocks are scheduled as tail items (e = -1) covering padded rows
+// that no expert owns.
+// ---------------------------------------------------------------------------
+struct Work {
+  int e;        // expert, or -1 for a tail block owned by no expert
+  int n_tile;
+  int m_block;
+};
+
+__device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM,
+                                         int ntiles, int host_blocks, bool tail, Work& w) {
+  int expert_blocks = gpo[E] / BM;
+  expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
+  const int total_blocks = tail ? host_blocks : expert_blocks;
+  const int total = total_blocks * ntiles;
+  const int per = (total + kNumXcd - 1) / kNumXcd;
+  const int slot = g / kNumXcd;
+  const int v = (g % kNumXcd) * per + slot;
+  if (slot >= per || v >= total) return false;
+  const int expert_items = expert_blocks * ntiles;
+  if (v >= expert_items) {
+    const int t = v - expert_items;
+    w.e = -1;
+    w.m_block = expert_blocks + t / ntiles;
+    w.n_tile = t % ntiles;
+    return true;
+  }
+  // e = (number of experts whose first item is <= v) - 1, found with ballots.
+  const int l = lane_id();
+  int cnt = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + l;
+    int le = 0;
+    if (e < E) le = (gpo[e] / BM) * ntiles <= v;
+    cnt += __popcll(__ballot(le));
+  }
+  const int e = cnt - 1;
+  if (e < 0) return false;  // only with inconsistent metadata (gpo[0] > 0)
+  const int b0 = gpo[e] / BM;
+  const int mb = gpo[e + 1] / BM - b0;
+  if (mb <= 0) return false;
+  const int local = v - b0 * ntiles;
+  w.e = e;
+  w.n_tile = local / mb;
+  w.m_block = b0 + local % mb;
+  return w.m_block >= 0 && w.m_block < host_blocks && w.n_tile < ntiles;
+}
+
+// Upper bound on the workgroups `schedule` needs for `blocks` M blocks.
+inline int64_t schedule_grid(int64_t blocks, int64_t ntiles) {
+  const int64_t total = blocks * ntiles;
+  const int64_t per = (total + kNumXcd - 1) / kNumXcd;
+  return per * kNumXcd;
+}
+
+}  // namespace moe

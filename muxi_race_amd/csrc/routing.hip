@@ -1,0 +1,301 @@
+// Router (softmax -> top-k -> renormalise), moe_align (expert-sorted,
+// block-padded permutation + group metadata), k-way combine, and per-row
+// int8 quantisation.  All integer outputs are deterministic: no result depends
+// on the order in which atomics land.
+#include "launch.h"
+#include "moe_common.h"
+
+#include <math.h>
+
+namespace moe {
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Router: one wave per token, VPL = ceil(E/64) logits per lane.
+// ---------------------------------------------------------------------------
+template <int VPL>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
+                                                         const float* __restrict__ bias, int T,
+                                                         int E, int k, int32_t* __restrict__ ids,
+                                                         float* __restrict__ wout) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = lane_id();
+  if (t >= T) return;  // uniform per wave
+  const float* row = logits + (int64_t)t * E;
+  float v[VPL];
+  uint32_t valid = 0;
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = l + 64 * j;
+    v[j] = -INFINITY;
+    if (e < E) {
+      float x = row[e];
+      if (bias) x = x + bias[e];
+      v[j] = x;
+      valid |= 1u << j;
+      m = fmaxf(m, x);
+    }
+  }
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (valid & (1u << j)) s += expf(v[j] - m);
+  s = wave_sum(s);
+
+  uint32_t taken = 0;
+  float my_p = 0.0f;
+  int my_id = 0;
+  float denom = 0.0f;
+  constexpr int kNone = 0x7fffffff;
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int be = kNone;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const uint32_t bit = 1u << j;
+      if ((valid & bit) && !(taken & bit) && (be == kNone || v[j] > bv)) {
+        bv = v[j];
+        be = l + 64 * j;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oe = __shfl_xor(be, o);
+      const bool take = oe != kNone && (be == kNone || ov > bv || (ov == bv && oe < be));
+      if (take) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if ((be & 63) == l) taken |= 1u << (be >> 6);
+    const float pr = expf(bv - m) / s;
+    denom = denom + pr;  // selection order, identical in every lane
+    if (l == r) {
+      my_p = pr;
+      my_id = be;
+    }
+  }
+  if (l < k) {
+    ids[(int64_t)t * k + l] = my_id;
+    wout[(int64_t)t * k + l] = my_p / denom;
+  }
+}
+
+hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
+                             int32_t* ids, float* w, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((T + 3) / 4), block(256);
+  const int vpl = (E + 63) / 64;
+  if (vpl <= 1) hipLaunchKernelGGL(route_topk_kernel<1>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+  else if (vpl <= 2) hipLaunchKernelGGL(route_topk_kernel<2>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+  else if (vpl <= 4) hipLaunchKernelGGL(route_topk_kernel<4>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+  else if (vpl <= 8) hipLaunchKernelGGL(route_topk_kernel<8>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+  else hipLaunchKernelGGL(route_topk_kernel<16>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// moe_align: one workgroup of 1024 threads (16 waves).
+//   1. LDS histogram of expert ids (order-free counts).
+//   2. Wave 0 scans counts -> group_offsets, padded counts -> padded offsets.
+//   3. Pairs are placed in chunks of 1024 in pair order.  Inside a wave, lanes
+//      holding the same expert are found by ANDing ballots of the expert-id
+//      bits; a lane's slot = expert cursor + same-expert pairs of earlier waves
+//      in the chunk + same-expert lanes below it.  Placement therefore follows
+//      pair order exactly, independent of timing.
+//   4. Sentinel rows and the block -> expert map.
+// ---------------------------------------------------------------------------
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / 64;
+
+__global__ __launch_bounds__(kAlignThreads) void align_kernel(
+    const int32_t* __restrict__ ids, int P, int E, int BM, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
+    int32_t* __restrict__ gpo) {
+  extern __shared__ int sm[];
+  int* cnt = sm;                 // [E]
+  int* cur = sm + E;             // [E] next free row of each expert
+  int* pstart = sm + 2 * E;      // [E+1] padded offsets
+  // [kAlignWaves][E] per-wave counts of this chunk (<= 64, so one byte each)
+  unsigned char* wc = reinterpret_cast<unsigned char*>(sm + 3 * E + 1);
+  const int tid = threadIdx.x, l = lane_id(), wave = tid >> 6;
+
+  for (int i = tid; i < E; i += kAlignThreads) cnt[i] = 0;
+  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wc[i] = 0;
+  __syncthreads();
+  for (int p = tid; p < P; p += kAlignThreads) {
+    const int e = ids[p];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[e], 1);  // out-of-range ids are dropped
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    int carry = 0, carry_p = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + l;
+      const int c = e < E ? cnt[e] : 0;
+      const int pc = (c + BM - 1) / BM * BM;
+      int ic = c, ip = pc;  // inclusive scans
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(ic, o), b = __shfl_up(ip, o);
+        if (l >= o) {
+          ic += a;
+          ip += b;
+        }
+      }
+      if (e < E) {
+        gs[e] = c;
+        go[e] = carry + ic - c;
+        gpo[e] = carry_p + ip - pc;
+        pstart[e] = carry_p + ip - pc;
+        cur[e] = carry_p + ip - pc;
+      }
+      carry += __shfl(ic, 63);
+      carry_p += __shfl(ip, 63);
+    }
+    if (l == 0) {
+      go[E] = carry;
+      gpo[E] = carry_p;
+      pstart[E] = carry_p;
+    }
+  }
+  __syncthreads();
+
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  for (int c0 = 0; c0 < P; c0 += kAlignThreads) {
+    const int p = c0 + tid;
+    int e = p < P ? ids[p] : -1;
+    const bool ok = (unsigned)e < (unsigned)E;
+    if (!ok) e = 0;
+    uint64_t same = __ballot(ok);
+    for (int b = 0; b < nbits; ++b) {
+      const int bit = (e >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      same &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(same & lt_mask);
+    const bool leader = ok && rank == 0;
+    const int n_same = __popcll(same);
+    if (leader) wc[wave * E + e] = (unsigned char)n_same;
+    __syncthreads();
+    if (ok) {
+      int prior = 0;
+      for (int w2 = 0; w2 < wave; ++w2) prior += (int)wc[w2 * E + e];
+      sorted_ids[cur[e] + prior + rank] = p;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&cur[e], n_same);
+      wc[wave * E + e] = 0;
+    }
+    __syncthreads();
+  }
+
+  // Padding rows -> sentinel P; blocks -> owning expert.
+  for (int e = wave; e < E; e += kAlignWaves) {
+    const int c = cnt[e];
+    const int lo = pstart[e] + c, hi = pstart[e + 1];
+    for (int r = lo + l; r < hi; r += 64) sorted_ids[r] = P;
+    for (int b = pstart[e] / BM + l; b < hi / BM; b += 64) block_expert[b] = e;
+  }
+}
+
+hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorted_ids,
+                        int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
+                        hipStream_t s) {
+  const size_t lds = sizeof(int) * (3 * (size_t)E + 1) + (size_t)kAlignWaves * E;
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), lds, s, ids, P, E, BM,
+                     sorted_ids, block_expert, gs, go, gpo);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Combine: out[t, :] = sum_j y_pair[t*k + j, :], fp32 in choice order -> fp16.
+// One thread per 8 output columns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y, int64_t T,
+                                                      int64_t H, int k, _Float16* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t cpr = H / 8;
+  if (idx >= T * cpr) return;
+  const int64_t t = idx / cpr, c = idx % cpr;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const _Float16* src = y + (t * k) * H + 8 * c;
+  for (int j = 0; j < k; ++j) {
+    const f16x8 v = *reinterpret_cast<const f16x8*>(src + (int64_t)j * H);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += (float)v[q];
+  }
+  f16x8 r;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) r[q] = (_Float16)acc[q];
+  *reinterpret_cast<f16x8*>(out + t * H + 8 * c) = r;
+}
+
+hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
+                          hipStream_t s) {
+  const int64_t n = T * (H / 8);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16*>(y_pair), T, H, k,
+                     reinterpret_cast<_Float16*>(out));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Per-row symmetric int8: one wave per row, 8 fp16 per lane per step.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ w, int64_t R,
+                                                         int64_t K, int8_t* __restrict__ q,
+                                                         float* __restrict__ scale) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = lane_id();
+  if (r >= R) return;
+  const _Float16* row = w + r * K;
+  float amax = 0.0f;
+  for (int64_t c = 8 * l; c < K; c += 512) {
+    const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
+  }
+  amax = wave_max(amax);
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int8_t* qrow = q + r * K;
+  for (int64_t c = 8 * l; c < K; c += 512) {
+    const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
+    u32x2 packed = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int qv = quant_i8((float)v[i], inv);
+      packed[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+    }
+    *reinterpret_cast<u32x2*>(qrow + c) = packed;
+  }
+  if (l == 0) scale[r] = amax / 127.0f;
+}
+
+hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+                             hipStream_t s) {
+  if (R == 0) return hipSuccess;
+  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16*>(w), R, K, q, scale);
+  return hipGetLastError();
+}
+
+}  // namespace moe

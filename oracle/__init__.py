@@ -1,0 +1,41 @@
+"""CPU oracle for the fused-MoE hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the algorithm of the reference's pre-routed
+fused expert MLP (problem_detail.json:50, xpuoj_data/race_stress2.py:29-48) plus
+the build-defined routing, alignment, combine and W8A8 steps that the reference
+does not implement.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or as
+the timed CPU baseline.  The product package ``muxi_race_amd`` never imports
+it: the HIP library is the only compute path.
+
+Pinning (how each function is checked independently of its own formula):
+
+* ``route_topk``        -- brute-force rank counting + scipy softmax closed form
+                           (tests/test_oracle_routing.py).
+* ``align`` / ``metadata_from_group_sizes`` -- hand-written known answers
+                           (problem_detail.json:40 example, RB:82-101 cases) and
+                           permutation/padding invariants (tests/test_oracle_align.py).
+* ``prerouted_forward`` -- permutation-matrix closed form (catches transposed
+                           operands and raw/padded index mix-ups), an fp64 scalar
+                           loop on tiny inputs, E=1 dense SwiGLU, zero-size
+                           experts, V=0, NaN-poisoned padding, power-of-two
+                           linearity (tests/test_oracle_core.py).
+* ``combine``           -- closed form on one-hot inputs (tests/test_oracle_core.py).
+* ``quantize_rows_int8`` / ``w8a8_forward`` -- exact integer checks on
+                           hand-made rows, round-half-away edge cases, and the
+                           fp16 oracle within the north-star W8A8 gate
+                           (tests/test_oracle_w8a8.py).
+"""
+
+from .moe_ref import (  # noqa: F401
+    route_topk,
+    align,
+    metadata_from_group_sizes,
+    prerouted_forward,
+    gather_rows,
+    combine,
+    fused_moe_forward,
+    quantize_rows_int8,
+    w8a8_forward,
+    silu_mul,
+)

@@ -1,0 +1,76 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what
+include/moe_gfx950.h declares (with matching arity), and host-side validation
+rejects bad arguments before any GPU call."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "moe_gfx950.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(moe_\w+)\s*\(([^;{]*?)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_header_declares_entry_points():
+    decl = _declared()
+    for name in ("moe_run_prerouted", "moe_route_topk", "moe_align", "moe_fused_forward",
+                 "moe_fused_forward_w8a8", "moe_quantize_rows_w8", "moe_last_error_string"):
+        assert name in decl
+
+
+def test_library_exports_every_declared_symbol():
+    from muxi_race_amd._lib import SIGNATURES, lib
+    L = lib()
+    decl = _declared()
+    assert set(decl) == set(SIGNATURES), set(decl) ^ set(SIGNATURES)
+    for name, arity in decl.items():
+        assert hasattr(L, name), name
+        assert len(SIGNATURES[name][1]) == arity, (name, arity)
+
+
+def test_host_validation_without_gpu():
+    from muxi_race_amd._lib import lib
+    L = lib()
+    assert L.moe_version() >= 1
+    nul = ctypes.c_void_p(0)
+    # P = 0 is a no-op (reference fast exit), no device access
+    rc = L.moe_run_prerouted(nul, nul, nul, nul, nul, 0, nul, nul, nul, nul, nul,
+                             0, 128, 128, 4, 0, 0, nul, 0, nul)
+    assert rc == 0
+    # H not a multiple of 128
+    rc = L.moe_run_prerouted(nul, nul, nul, nul, nul, 0, nul, nul, nul, nul, nul,
+                             128, 100, 128, 4, 10, 1, nul, 0, nul)
+    assert rc == -2 and b"multiples of 128" in L.moe_last_error_string()
+    # null pointers
+    rc = L.moe_run_prerouted(nul, nul, nul, nul, nul, 0, nul, nul, nul, nul, nul,
+                             128, 128, 128, 4, 10, 1, nul, 0, nul)
+    assert rc == -1
+    rc = L.moe_route_topk(nul, nul, 4, 2000, 2, nul, nul, nul)
+    assert rc == -2
+    rc = L.moe_fused_forward(nul, nul, nul, nul, nul, nul, nul, 4, 128, 128, 8, 2, 48,
+                             nul, 0, nul, nul, nul)
+    assert rc == -2 and b"block_m" in L.moe_last_error_string()
+    rc = L.moe_quantize_rows_w8(nul, 4, 12, nul, nul, nul)
+    assert rc == -1
+
+
+def test_capacity_and_workspace_sizes():
+    from muxi_race_amd._lib import lib
+    L = lib()
+    # P + min(E, P) * (bm - 1), rounded down to whole blocks
+    assert L.moe_align_capacity_rows(4096, 8, 256, 128) == (32768 + 256 * 127) // 128 * 128
+    assert L.moe_align_capacity_rows(1, 1, 256, 32) == 32
+    assert L.moe_prerouted_workspace_bytes(256, 512) == 256 * 512 * 2
+    assert L.moe_pick_block_m(4096, 256, 8) == 128
+    assert L.moe_pick_block_m(32, 256, 8) == 32
+    ws = L.moe_fused_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 0)
+    assert ws >= 32768 * 7168 * 2 + 65280 * 2048 * 2

@@ -1,0 +1,79 @@
+"""GPU router and moe_align: indices bit-exact against the CPU oracle on every
+BASELINE config's logits and on tie-heavy / edge inputs."""
+import numpy as np
+import pytest
+import torch
+
+from _cases import CONFIGS, moe_inputs
+from oracle import align, route_topk
+
+pytestmark = pytest.mark.gpu
+
+
+def _route_both(logits, k, bias):
+    from muxi_race_amd import route_topk as gpu_route
+    ids, w = gpu_route(logits, k, bias)
+    torch.cuda.synchronize()
+    rid, rw = route_topk(logits.cpu().numpy(), k, None if bias is None else bias.cpu().numpy())
+    return ids.cpu().numpy(), w.cpu().numpy(), rid, rw
+
+
+def _logits_for(name, seed):
+    T, H, I, E, k, bias_kind = CONFIGS[name]
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn((T, E), generator=g)
+    bias = None
+    if bias_kind == "normal":
+        bias = torch.randn((E,), generator=g) * 0.5
+    elif bias_kind == "zipf":
+        bias = -1.2 * torch.log(torch.arange(E, dtype=torch.float32) + 1)
+    return logits.cuda(), (None if bias is None else bias.cuda()), k, E
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_routing_bit_exact(name):
+    logits, bias, k, E = _logits_for(name, 100)
+    ids, w, rid, rw = _route_both(logits, k, bias)
+    np.testing.assert_array_equal(ids, rid)
+    np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (256, 8), (1000, 32), (3, 3)])
+def test_routing_ties(E, k):
+    g = torch.Generator().manual_seed(E)
+    logits = (torch.randn((257, E), generator=g) * 2).round() / 2  # many exact ties
+    logits[0] = 0.0  # all-equal row -> experts 0..k-1
+    ids, w, rid, rw = _route_both(logits.cuda(), k, None)
+    np.testing.assert_array_equal(ids, rid)
+    np.testing.assert_array_equal(ids[0], np.arange(k))
+    np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
+
+
+def _align_both(ids_np, E, bm):
+    from muxi_race_amd import moe_align
+    got = moe_align(torch.from_numpy(ids_np).cuda(), E, bm)
+    torch.cuda.synchronize()
+    ref = align(ids_np, E, bm)
+    rows = int(ref["group_padded_offsets"][-1])
+    assert int(got["group_padded_offsets"][-1]) == rows
+    np.testing.assert_array_equal(got["sorted_pair_ids"][:rows].cpu().numpy(), ref["sorted_pair_ids"])
+    np.testing.assert_array_equal(got["block_expert"][:rows // bm].cpu().numpy(), ref["block_expert"])
+    for key in ("group_sizes", "group_offsets", "group_padded_offsets"):
+        np.testing.assert_array_equal(got[key].cpu().numpy(), ref[key])
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+@pytest.mark.parametrize("bm", [32, 128])
+def test_align_bit_exact(name, bm):
+    logits, bias, k, E = _logits_for(name, 200)
+    rid, _ = route_topk(logits.cpu().numpy(), k, None if bias is None else bias.cpu().numpy())
+    _align_both(rid, E, bm)
+
+
+def test_align_edges():
+    rng = np.random.default_rng(0)
+    _align_both(np.zeros((3000, 1), np.int32), 4, 128)            # one expert takes all
+    _align_both(np.array([[5]], np.int32), 1024, 64)              # one pair, E = 1024
+    _align_both(np.zeros((0, 2), np.int32), 8, 128)               # no tokens
+    ids = np.stack([rng.choice(1024, 8, replace=False) for _ in range(5000)]).astype(np.int32)
+    _align_both(ids, 1024, 32)                                     # many chunks, wide E

@@ -1,0 +1,181 @@
+"""Pins oracle.prerouted_forward / combine / fused_moe_forward
+(problem_detail.json:50 semantics) without retyping its formula."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import combine, fused_moe_forward, metadata_from_group_sizes, prerouted_forward, route_topk
+
+
+def _silu(v):
+    return v / (1.0 + math.exp(-v))
+
+
+def _perm_matrix(perm):
+    n = len(perm)
+    m = np.zeros((n, n), dtype=np.float32)
+    for i, p in enumerate(perm):
+        m[i, p] = 1.0  # (x M^T)[i] = x[perm[i]]
+    return m
+
+
+def test_permutation_closed_form():
+    """Wg = a*Pg, Wu = b*Pu, Wd = c*Pd with non-involutive permutations:
+    out[r, j] = routed[go[e]+i] * c * silu(a*x[pg[pd[j]]]) * b*x[pu[pd[j]]].
+    A transposed operand, a dropped factor or a padded/raw index mix-up changes
+    the result."""
+    n = 8
+    sizes = [3, 0, 2, 5]
+    E = len(sizes)
+    go, gpo, gidx = metadata_from_group_sizes(sizes, 128)
+    P = int(gpo[-1])
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((P, n)).astype(np.float16)
+    perms = {}
+    wg = np.zeros((E, n, n), np.float16)
+    wu = np.zeros((E, n, n), np.float16)
+    wd = np.zeros((E, n, n), np.float16)
+    coef = [(0.5, 2.0, 0.25), (1.0, 1.0, 1.0), (2.0, 0.5, 1.5), (0.75, -1.0, 0.5)]
+    for e in range(E):
+        pg = [(i + 1 + e) % n for i in range(n)]
+        pu = [(3 * i + 2) % n for i in range(n)]
+        pd = [(5 * i + e) % n for i in range(n)]
+        perms[e] = (pg, pu, pd)
+        a, b, c = coef[e]
+        wg[e] = a * _perm_matrix(pg)
+        wu[e] = b * _perm_matrix(pu)
+        wd[e] = c * _perm_matrix(pd)
+    V = int(go[-1])
+    routed = (1.0 + 0.125 * np.arange(V)).astype(np.float32)
+    out = prerouted_forward(x, wg, wu, wd, routed, sizes, go, gpo, gidx, out_fp32=True).numpy()
+    exp = np.zeros((P, n), np.float64)
+    for e in range(E):
+        pg, pu, pd = perms[e]
+        a, b, c = coef[e]
+        for i in range(sizes[e]):
+            r = gpo[e] + i
+            xr = x[r].astype(np.float64)
+            for j in range(n):
+                hi = pd[j]
+                exp[r, j] = routed[go[e] + i] * c * _silu(a * xr[pg[hi]]) * (b * xr[pu[hi]])
+    np.testing.assert_allclose(out, exp, rtol=2e-6, atol=1e-7)
+
+
+def test_scalar_loop_fp64(rng):
+    """Random tiny case against a plain fp64 triple loop."""
+    H, I, sizes = 6, 5, [2, 1, 0, 3]
+    E = len(sizes)
+    go, gpo, gidx = metadata_from_group_sizes(sizes, 128)
+    P = int(gpo[-1])
+    x = rng.standard_normal((P, H)).astype(np.float16)
+    wg = (rng.standard_normal((E, I, H)) * 0.5).astype(np.float16)
+    wu = (rng.standard_normal((E, I, H)) * 0.5).astype(np.float16)
+    wd = (rng.standard_normal((E, H, I)) * 0.5).astype(np.float16)
+    routed = rng.random(int(go[-1])).astype(np.float16)
+    out = prerouted_forward(x, wg, wu, wd, routed, sizes, go, gpo, gidx, out_fp32=True).numpy()
+    for e in range(E):
+        for i in range(sizes[e]):
+            r = gpo[e] + i
+            xr = [float(v) for v in x[r]]
+            h = []
+            for q in range(I):
+                g = sum(xr[k] * float(wg[e, q, k]) for k in range(H))
+                u = sum(xr[k] * float(wu[e, q, k]) for k in range(H))
+                h.append(_silu(g) * u)
+            for j in range(H):
+                y = sum(h[q] * float(wd[e, j, q]) for q in range(I)) * float(routed[go[e] + i])
+                assert abs(out[r, j] - y) <= 1e-5 * (1 + abs(y))
+    mask = np.ones(P, bool)
+    for e in range(E):
+        mask[gpo[e]:gpo[e] + sizes[e]] = False
+    assert (out[mask] == 0).all()
+
+
+def test_single_expert_is_dense_swiglu(rng):
+    H, I, n = 16, 24, 100
+    go, gpo, gidx = metadata_from_group_sizes([n], 128)
+    x = torch.from_numpy(rng.standard_normal((128, H)).astype(np.float16))
+    wg = torch.from_numpy((rng.standard_normal((1, I, H)) * 0.3).astype(np.float16))
+    wu = torch.from_numpy((rng.standard_normal((1, I, H)) * 0.3).astype(np.float16))
+    wd = torch.from_numpy((rng.standard_normal((1, H, I)) * 0.3).astype(np.float16))
+    routed = torch.ones(n)
+    out = prerouted_forward(x, wg, wu, wd, routed, [n], go, gpo, gidx, out_fp32=True)
+    xd = x[:n].double()
+    dense = (torch.nn.functional.silu(xd @ wg[0].double().T) * (xd @ wu[0].double().T)) @ wd[0].double().T
+    torch.testing.assert_close(out[:n].double(), dense, rtol=1e-5, atol=1e-6)
+    assert (out[n:] == 0).all()
+
+
+def test_nan_padding_and_empty_cases(rng):
+    H, I, sizes = 8, 8, [1, 0, 127]
+    go, gpo, gidx = metadata_from_group_sizes(sizes, 128)
+    P = int(gpo[-1])
+    x = rng.standard_normal((P, H)).astype(np.float16)
+    pad = np.ones(P, bool)
+    for e, n in enumerate(sizes):
+        pad[gpo[e]:gpo[e] + n] = False
+    x[pad] = np.nan
+    w = (rng.standard_normal((3, I, H)) * 0.2).astype(np.float16)
+    wdn = (rng.standard_normal((3, H, I)) * 0.2).astype(np.float16)
+    routed = rng.random(int(go[-1])).astype(np.float32)
+    out = prerouted_forward(x, w, w, wdn, routed, sizes, go, gpo, gidx)
+    assert torch.isfinite(out).all()
+    assert (out[torch.from_numpy(pad)] == 0).all()
+    # V = 0: every row is padding
+    go0, gpo0, gidx0 = metadata_from_group_sizes([0, 0, 0], 128)
+    out0 = prerouted_forward(np.zeros((0, H), np.float16), w, w, wdn, np.zeros(0, np.float32), [0, 0, 0], go0, gpo0, gidx0)
+    assert out0.shape == (0, H)
+
+
+def test_routed_weight_linearity(rng):
+    H, I, sizes = 16, 16, [5, 9]
+    go, gpo, gidx = metadata_from_group_sizes(sizes, 128)
+    P = int(gpo[-1])
+    x = rng.standard_normal((P, H)).astype(np.float16)
+    wg = (rng.standard_normal((2, I, H)) * 0.2).astype(np.float16)
+    wd = (rng.standard_normal((2, H, I)) * 0.2).astype(np.float16)
+    r = rng.random(14).astype(np.float32)
+    # fp32 output: scaling by 2 is exact (fp16 subnormals would round differently)
+    o1 = prerouted_forward(x, wg, wg, wd, r, sizes, go, gpo, gidx, out_fp32=True)
+    o2 = prerouted_forward(x, wg, wg, wd, 2 * r, sizes, go, gpo, gidx, out_fp32=True)
+    torch.testing.assert_close(o2, 2 * o1, rtol=0, atol=0)
+
+
+def test_combine_closed_form():
+    T, k, H = 3, 2, 4
+    y = torch.zeros(T * k, H)
+    for p in range(T * k):
+        y[p, p % H] = float(p + 1)
+    out = combine(y, T, k)
+    exp = torch.zeros(T, H)
+    for t in range(T):
+        for j in range(k):
+            p = t * k + j
+            exp[t, p % H] += p + 1
+    torch.testing.assert_close(out, exp, rtol=0, atol=0)
+
+
+def test_fused_matches_dense_per_token(rng):
+    """Full pipeline (route -> align -> gather -> grouped MLP -> combine) against
+    a per-token dense formulation in fp64 that never sorts or pads."""
+    T, H, I, E, k = 40, 32, 16, 6, 2
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16))
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32))
+    wg = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wu = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wd = torch.from_numpy((rng.standard_normal((E, H, I)) * 0.2).astype(np.float16))
+    for bm in (32, 128):
+        out = fused_moe_forward(x, logits, wg, wu, wd, k, bias, block_m=bm)
+        ids, w = route_topk(logits.numpy(), k, bias.numpy())
+        exp = torch.zeros(T, H, dtype=torch.float64)
+        for t in range(T):
+            xt = x[t].double()
+            for j in range(k):
+                e = int(ids[t, j])
+                g = wg[e].double() @ xt
+                u = wu[e].double() @ xt
+                exp[t] += float(w[t, j]) * (wd[e].double() @ (torch.sigmoid(g) * g * u))
+        torch.testing.assert_close(out.double(), exp, rtol=2e-3, atol=2e-3)

@@ -132,6 +132,9 @@ def main():
     ap.add_argument("--block-m", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the sampled oracle check")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
+                         "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -223,10 +226,26 @@ def main():
                                 inp["wd"], k, None if inp["bias"] is None else inp["bias"].cpu()).float()
         got = out[r].float().cpu()
         ok = bool(torch.isfinite(got).all()) and bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
-        check_res = dict(routing_ids_bit_exact=ids_ok, sampled_tokens=len(rows),
-                         within_rtol2e-2_atol1e-2=ok)
+        check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
+                     "within_rtol2e-2_atol1e-2": ok}
 
     cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
+
+    copy_gbs = None
+    if args.calib_copy:
+        n = 1 << 29  # 1 GiB of fp16 read + 1 GiB written per copy
+        src = torch.empty(n, dtype=torch.float16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(3):
+            dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        copy_gbs = round(4 * n / (a.elapsed_time(b) / 3 * 1e-3) / 1e9, 1)  # read + write
+        del src, dst
 
     res = {
         "metric": METRIC,
@@ -268,6 +287,8 @@ def main():
         "check": check_res,
         "wall_ms_timed_region": round(wall_ms, 2),
     }
+    if copy_gbs is not None:
+        res["calib_copy_gb_per_s"] = copy_gbs
     print(json.dumps(res), flush=True)
 
 

@@ -41,8 +41,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (need ROCm with gfx950 support)")
 
 
-def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, extra=()) -> tuple[Path, str]:
+    cmd = [_hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(
         ln for ln in (r.stdout + r.stderr).splitlines()
@@ -53,28 +53,34 @@ def _compile(src: Path, obj: Path) -> tuple[Path, str]:
     return obj, msgs
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip and link the shared library; returns its path."""
-    OBJDIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, defines: dict | None = None, out: Path | None = None) -> Path:
+    """Compile every csrc/*.hip and link the shared library; returns its path.
+
+    ``defines`` adds -DNAME=VALUE tuning macros (e.g. MOE_S2_STAGES_128) and
+    ``out`` redirects the library (default: muxi_race_amd/libmoe_gfx950.so)."""
+    lib = LIB if out is None else Path(out)
+    objdir = OBJDIR if out is None else lib.parent / "_build"
+    objdir.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{k}={v}" for k, v in (defines or {}).items()]
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources in {CSRC}")
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_compile, s, OBJDIR / (s.stem + ".o")) for s in srcs]
+        futs = [ex.submit(_compile, s, objdir / (s.stem + ".o"), extra) for s in srcs]
         objs = []
         for f in futs:
             obj, msgs = f.result()
             objs.append(obj)
             if verbose and msgs.strip():
                 print(msgs, file=sys.stderr)
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":

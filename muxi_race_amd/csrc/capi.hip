@@ -51,7 +51,7 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, 
   L.go = o; o += up((E + 1) * 4);
   L.gpo = o; o += up((E + 1) * 4);
   L.h = o; o += up(rows * I * (w8 ? 1 : 2));
-  L.hs = o; o += w8 ? up(rows * (I / moe::kBN) * 4) : 0;
+  L.hs = o; o += w8 ? up(rows * (I / moe::kBN) * 4) : 0;  // [I/128][rows], block-major
   L.xq = o; o += w8 ? up(T * H) : 0;
   L.sx = o; o += w8 ? up(T * 4) : 0;
   L.ypair = o; o += up(P * H * 2);
@@ -220,6 +220,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const float
   p1.wu = (const char*)wu;
   p1.h = ws + L.h;
   p1.h_scale = w8 ? (float*)(ws + L.hs) : nullptr;
+  p1.hs_stride = rows;
   p1.x_scale = w8 ? (const float*)(ws + L.sx) : nullptr;
   p1.sg = sg;
   p1.su = su;
@@ -236,6 +237,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const float
   moe::Stage2Params p2{};
   p2.a = ws + L.h;
   p2.a_scale = w8 ? (const float*)(ws + L.hs) : nullptr;
+  p2.as_stride = rows;
   p2.wd = (const char*)wd;
   p2.sd = sd;
   p2.out = ws + L.ypair;

@@ -6,10 +6,10 @@
 // :1391-1635) and Stage2 family (:655-795, :1132-1378); base form
 // xpuoj_data/submission.py:31-129 and :253-331.  The tiling here is this
 // build's own: a 256-thread workgroup computes a BM x 128 output tile (Stage 1:
-// for gate and up at once, sharing the token tile), K advances 128 bytes per
-// step through a double-buffered, XOR-swizzled LDS tile that is filled from a
-// register prefetch of the next step, so global loads of step k+1 overlap the
-// MFMAs of step k with one barrier per step.
+// for gate and up at once, sharing the token tile); K advances 128 bytes per
+// step through an S-stage ring of XOR-swizzled LDS tiles filled by direct
+// global->LDS loads (global_load_lds_dwordx4), so S-2 steps of loads stay in
+// flight behind the MFMAs of the current step, with one barrier per step.
 #include "launch.h"
 #include "moe_common.h"
 
@@ -27,14 +27,15 @@ struct Layout {
   static_assert(NBM >= 1 && NBN >= 1, "wave tile must hold at least one 32x32 block");
 };
 
-template <int BM, int WAVES_M, bool I8, bool GATHER>
+template <int BM, int WAVES_M, int S, bool I8, bool GATHER>
 __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   using L = Layout<BM, WAVES_M>;
   using Acc = typename std::conditional<I8, i32x16, f32x16>::type;
   constexpr int XB = BM * kRowBytes;
   constexpr int WB = kBN * kRowBytes;
   constexpr int STAGE = XB + 2 * WB;
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
+  __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
   const int ntiles = (int)(p.I / kBN);
   Work w;
@@ -50,11 +51,11 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
 
-  TileLoader<BM> xl;
-  TileLoader<kBN> gl, ul;
+  DmaTile<BM> xl;
+  DmaTile<kBN> gl, ul;
 #pragma unroll
-  for (int i = 0; i < TileLoader<BM>::CH; ++i) {
-    const int r = TileLoader<BM>::row_of(i);
+  for (int i = 0; i < DmaTile<BM>::NI; ++i) {
+    const int r = DmaTile<BM>::row_of(i);
     int64_t src_row;
     if (GATHER) {
       const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
@@ -67,8 +68,8 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const char* gbase = p.wg + ((int64_t)e * p.I + n0) * kbytes;
   const char* ubase = p.wu + ((int64_t)e * p.I + n0) * kbytes;
 #pragma unroll
-  for (int i = 0; i < TileLoader<kBN>::CH; ++i) {
-    const int r = TileLoader<kBN>::row_of(i);
+  for (int i = 0; i < DmaTile<kBN>::NI; ++i) {
+    const int r = DmaTile<kBN>::row_of(i);
     gl.set(i, gbase + r * kbytes);
     ul.set(i, ubase + r * kbytes);
   }
@@ -85,50 +86,54 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
       au[a][b] = Acc{};
     }
 
-  xl.load(0);
-  gl.load(0);
-  ul.load(0);
-  xl.store(smem);
-  gl.store(smem + XB);
-  ul.store(smem + XB + WB);
-  __syncthreads();
-
+  // S-stage ring: stages ks+1 .. ks+S-2 stay in flight while stage ks is used.
+  constexpr int Q = DmaTile<BM>::NI + 2 * DmaTile<kBN>::NI;  // loads per wave per stage
+  auto issue = [&](int buf, int k) {
+    char* st = smem + buf * STAGE;
+    xl.issue(st, k);
+    gl.issue(st + XB, k);
+    ul.issue(st + XB + WB, k);
+  };
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s, s);
+  int cur = 0;
   for (int ks = 0; ks < nk; ++ks) {
-    const char* cx = smem + (ks & 1) * STAGE;
+    wait_stages<Q, S - 2>(nk - 1 - ks);
+    barrier_no_fence();
+    if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
+    const char* cx = smem + cur * STAGE;
     const char* cg = cx + XB;
     const char* cu = cg + WB;
-    const bool more = ks + 1 < nk;
-    if (more) {
-      xl.load(ks + 1);
-      gl.load(ks + 1);
-      ul.load(ks + 1);
-    }
+    cur = cur + 1 == S ? 0 : cur + 1;
+    // Fragments are double-buffered across the 4 K sub-steps so the LDS reads
+    // of sub-step s+1 are in flight while the MFMAs of sub-step s run.
+    u32x4 xf[2][L::NBM], gf[2][L::NBN], uf[2][L::NBN];
+    auto load_frags = [&](int buf, int s) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4 xf[L::NBM], gf[L::NBN], uf[L::NBN];
-#pragma unroll
-      for (int b = 0; b < L::NBM; ++b) xf[b] = frag(cx, wm * L::WTM + 32 * b, s);
+      for (int b = 0; b < L::NBM; ++b) xf[buf][b] = frag(cx, wm * L::WTM + 32 * b, s);
 #pragma unroll
       for (int a = 0; a < L::NBN; ++a) {
-        gf[a] = frag(cg, wn * L::WTN + 32 * a, s);
-        uf[a] = frag(cu, wn * L::WTN + 32 * a, s);
+        gf[buf][a] = frag(cg, wn * L::WTN + 32 * a, s);
+        uf[buf][a] = frag(cu, wn * L::WTN + 32 * a, s);
       }
+    };
+    load_frags(0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int fb = s & 1;
+      if (s < 3) load_frags(fb ^ 1, s + 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
       for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
         for (int b = 0; b < L::NBM; ++b) {
-          ag[a][b] = mma(gf[a], xf[b], ag[a][b]);
-          au[a][b] = mma(uf[a], xf[b], au[a][b]);
+          ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
+          au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
         }
     }
-    if (more) {
-      char* nx = smem + ((ks + 1) & 1) * STAGE;
-      xl.store(nx);
-      gl.store(nx + XB);
-      ul.store(nx + XB + WB);
-    }
-    __syncthreads();
   }
+  __syncthreads();  // every wave is done with the ring before LDS is reused
 
   const int l = lane_id();
   if constexpr (!I8) {
@@ -185,7 +190,6 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
       if (l < 32) red[wn * BM + wm * L::WTM + 32 * b + l] = amax;
     }
     __syncthreads();
-    const int sblocks = (int)(p.I / kBN);
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
       const int mrow = wm * L::WTM + 32 * b + (l & 31);
@@ -209,19 +213,21 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
             }
             *reinterpret_cast<uint32_t*>(hrow + n) = packed;
           }
-        if (wn == 0 && l < 32) p.h_scale[grow * sblocks + w.n_tile] = amax / 127.0f;
+        // scales are stored block-major: [I/128][hs_stride]
+        if (wn == 0 && l < 32) p.h_scale[(int64_t)w.n_tile * p.hs_stride + grow] = amax / 127.0f;
       }
     }
   }
 }
 
-template <int BM, int WAVES_M, bool I8, bool FUSED>
+template <int BM, int WAVES_M, int S, bool I8, bool FUSED>
 __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
   using L = Layout<BM, WAVES_M>;
   constexpr int XB = BM * kRowBytes;
   constexpr int WB = kBN * kRowBytes;
-  constexpr int STAGE = XB + WB;
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  constexpr int STAGE = XB + WB + (I8 ? 1024 : 0);  // int8: + row scales of the step
+  static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
+  __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
   const int ntiles = (int)(p.H / kBN);
   Work w;
@@ -250,14 +256,14 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
 
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
-  TileLoader<BM> al;
-  TileLoader<kBN> wl;
+  DmaTile<BM> al;
+  DmaTile<kBN> wl;
 #pragma unroll
-  for (int i = 0; i < TileLoader<BM>::CH; ++i)
-    al.set(i, p.a + (int64_t)(row0 + TileLoader<BM>::row_of(i)) * kbytes);
+  for (int i = 0; i < DmaTile<BM>::NI; ++i)
+    al.set(i, p.a + (int64_t)(row0 + DmaTile<BM>::row_of(i)) * kbytes);
   const char* wbase = p.wd + ((int64_t)e * p.H + n0) * kbytes;
 #pragma unroll
-  for (int i = 0; i < TileLoader<kBN>::CH; ++i) wl.set(i, wbase + TileLoader<kBN>::row_of(i) * kbytes);
+  for (int i = 0; i < DmaTile<kBN>::NI; ++i) wl.set(i, wbase + DmaTile<kBN>::row_of(i) * kbytes);
 
   const int wave = threadIdx.x >> 6;
   const int wm = wave / L::WAVES_N;
@@ -269,63 +275,77 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) acc[a][b] = f32x16{};
 
-  const float* srow[L::NBM];
+  // int8: the row scales of K step ks (block-major layout, so contiguous) ride
+  // in the same stage: wave w loads rows 64w..64w+63 (clamped inside the tile)
+  // with one dword DMA, so every wave issues the same number of loads.
+  const float* scale_src = nullptr;
   if constexpr (I8) {
-    const int sblocks = (int)(p.I / kBN);
-#pragma unroll
-    for (int b = 0; b < L::NBM; ++b)
-      srow[b] = p.a_scale + (int64_t)(row0 + wm * L::WTM + 32 * b + (l & 31)) * sblocks;
+    const int r = 64 * wave_id() + l;
+    scale_src = p.a_scale + row0 + (r < BM ? r : 0);
   }
-
-  al.load(0);
-  wl.load(0);
-  al.store(smem);
-  wl.store(smem + XB);
-  __syncthreads();
-
+  constexpr int Q = DmaTile<BM>::NI + DmaTile<kBN>::NI + (I8 ? 1 : 0);
+  auto issue = [&](int buf, int k) {
+    char* st = smem + buf * STAGE;
+    al.issue(st, k);
+    wl.issue(st + XB, k);
+    if constexpr (I8)
+      dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + XB + WB + 256 * wave_id());
+  };
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s, s);
+  int cur = 0;
   for (int ks = 0; ks < nk; ++ks) {
-    const char* ca = smem + (ks & 1) * STAGE;
+    wait_stages<Q, S - 2>(nk - 1 - ks);
+    barrier_no_fence();
+    if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
+    const char* ca = smem + cur * STAGE;
     const char* cw = ca + XB;
-    const bool more = ks + 1 < nk;
-    if (more) {
-      al.load(ks + 1);
-      wl.load(ks + 1);
-    }
+    cur = cur + 1 == S ? 0 : cur + 1;
+    // Fragments double-buffered across the K sub-steps (see Stage 1).
+    u32x4 af[2][L::NBM], wf[2][L::NBN];
+    auto load_frags = [&](int buf, int s) {
+#pragma unroll
+      for (int b = 0; b < L::NBM; ++b) af[buf][b] = frag(ca, wm * L::WTM + 32 * b, s);
+#pragma unroll
+      for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(cw, wn * L::WTN + 32 * a, s);
+    };
     if constexpr (!I8) {
+      load_frags(0, 0);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        u32x4 af[L::NBM], wf[L::NBN];
-#pragma unroll
-        for (int b = 0; b < L::NBM; ++b) af[b] = frag(ca, wm * L::WTM + 32 * b, s);
-#pragma unroll
-        for (int a = 0; a < L::NBN; ++a) wf[a] = frag(cw, wn * L::WTN + 32 * a, s);
+        const int fb = s & 1;
+        if (s < 3) load_frags(fb ^ 1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
         for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-          for (int b = 0; b < L::NBM; ++b) acc[a][b] = mma(wf[a], af[b], acc[a][b]);
+          for (int b = 0; b < L::NBM; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
       }
     } else {
       // One K step of int8 is one 128-column scale block of the intermediate:
       // exact int32 partial product, then acc += partial * s_h[row, block].
+      const float* scl = reinterpret_cast<const float*>(cw + WB);
       float sc[L::NBM];
 #pragma unroll
-      for (int b = 0; b < L::NBM; ++b) sc[b] = srow[b][ks];
+      for (int b = 0; b < L::NBM; ++b) sc[b] = scl[wm * L::WTM + 32 * b + (l & 31)];
       i32x16 ia[L::NBN][L::NBM];
 #pragma unroll
       for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
         for (int b = 0; b < L::NBM; ++b) ia[a][b] = i32x16{};
+      load_frags(0, 0);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        u32x4 af[L::NBM], wf[L::NBN];
-#pragma unroll
-        for (int b = 0; b < L::NBM; ++b) af[b] = frag(ca, wm * L::WTM + 32 * b, s);
-#pragma unroll
-        for (int a = 0; a < L::NBN; ++a) wf[a] = frag(cw, wn * L::WTN + 32 * a, s);
+        const int fb = s & 1;
+        if (s < 3) load_frags(fb ^ 1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
         for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-          for (int b = 0; b < L::NBM; ++b) ia[a][b] = mma(wf[a], af[b], ia[a][b]);
+          for (int b = 0; b < L::NBM; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
       }
 #pragma unroll
       for (int a = 0; a < L::NBN; ++a)
@@ -334,12 +354,6 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
     }
-    if (more) {
-      char* nx = smem + ((ks + 1) & 1) * STAGE;
-      al.store(nx);
-      wl.store(nx + XB);
-    }
-    __syncthreads();
   }
 
   _Float16* o = reinterpret_cast<_Float16*>(p.out);
@@ -386,14 +400,47 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
   }
 }
 
+// LDS ring depth per tile: as many stages as fit the CU's 160 KiB (one
+// workgroup per CU for the wide tiles) -- the stages in flight are what keeps
+// enough bytes outstanding to stream weights at HBM rate.
+// Compile-time tunables (-D...) with the measured defaults.
+#ifndef MOE_S1_STAGES_128
+#define MOE_S1_STAGES_128 3
+#endif
+#ifndef MOE_S1_STAGES_64
+#define MOE_S1_STAGES_64 3
+#endif
+#ifndef MOE_S1_STAGES_32
+#define MOE_S1_STAGES_32 4
+#endif
+#ifndef MOE_S2_STAGES_128
+#define MOE_S2_STAGES_128 2
+#endif
+#ifndef MOE_S2_STAGES_64
+#define MOE_S2_STAGES_64 4
+#endif
+#ifndef MOE_S2_STAGES_32
+#define MOE_S2_STAGES_32 4
+#endif
+constexpr int s1_stages(int bm) {
+  return bm == 128 ? MOE_S1_STAGES_128 : (bm == 64 ? MOE_S1_STAGES_64 : MOE_S1_STAGES_32);
+}
+constexpr int s2_stages(int bm) {
+  return bm == 128 ? MOE_S2_STAGES_128 : (bm == 64 ? MOE_S2_STAGES_64 : MOE_S2_STAGES_32);
+}
+
 template <int BM, int WM, bool I8, bool GATHER>
 static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
-  hipLaunchKernelGGL((stage1_kernel<BM, WM, I8, GATHER>), dim3((unsigned)grid), dim3(kThreads), 0, s, p);
+  constexpr int kS = s1_stages(BM);
+  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, I8, GATHER>), dim3((unsigned)grid), dim3(kThreads),
+                     0, s, p);
   return hipGetLastError();
 }
 template <int BM, int WM, bool I8, bool FUSED>
 static hipError_t go2(const Stage2Params& p, int64_t grid, hipStream_t s) {
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, I8, FUSED>), dim3((unsigned)grid), dim3(kThreads), 0, s, p);
+  constexpr int kS = s2_stages(BM);
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, kS, I8, FUSED>), dim3((unsigned)grid), dim3(kThreads),
+                     0, s, p);
   return hipGetLastError();
 }
 

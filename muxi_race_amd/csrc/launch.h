@@ -12,7 +12,8 @@ struct Stage1Params {
   const char* wg;           // [E, I, H]
   const char* wu;           // [E, I, H]
   char* h;                  // fp16|int8 [padded rows, I]
-  float* h_scale;           // int8 only: [padded rows, I/128]
+  float* h_scale;           // int8 only: [I/128][hs_stride] (block-major)
+  int64_t hs_stride;        // int8 only: rows of each h_scale block (>= padded rows)
   const float* x_scale;     // int8 only: [T]
   const float* sg;          // int8 only: [E, I]
   const float* su;          // int8 only: [E, I]
@@ -29,7 +30,8 @@ struct Stage1Params {
 // Stage 2: y = h Wd^T, scaled by the routing weight of each row.
 struct Stage2Params {
   const char* a;            // fp16|int8 [padded rows, I]
-  const float* a_scale;     // int8 only: [padded rows, I/128]
+  const float* a_scale;     // int8 only: [I/128][as_stride] (block-major)
+  int64_t as_stride;        // int8 only: rows of each a_scale block (>= padded rows)
   const char* wd;           // [E, H, I]
   const float* sd;          // int8 only: [E, H]
   char* out;                // pre-routed: fp16 [P, H]; fused: fp16 [T*topk, H]

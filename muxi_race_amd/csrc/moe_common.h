@@ -39,10 +39,99 @@ constexpr float kLog2e = 1.44269504088896341f;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-// LDS byte offset of 16-byte chunk c of tile row r.
+// LDS byte offset of 16-byte chunk c of tile row r.  gfx950 serves a
+// ds_read_b128 16 lanes at a time across 64 four-byte banks: a fragment read
+// (16 consecutive rows, one chunk) is conflict-free when the 16 (row parity,
+// chunk slot) pairs are distinct, i.e. when the slot is c ^ f(r) with f taking
+// 8 distinct values over the even rows and over the odd rows of any 16-row
+// group.  f(r) = (r >> 1) & 7 does that (f(r) = r & 7 puts rows r and r + 8 on
+// the same banks: a 2-way conflict on every read, measured).
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int lds_swz(int r, int c) {
-  return (r << 7) | (((c ^ r) & 7) << 4);
+  return (r << 7) | (((c ^ swz(r)) & 7) << 4);
 }
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Pipelines issue Q loads per wave per stage, in stage order, and vector-memory
+// loads retire in order: waiting until at most Q*min(ahead, N) loads are
+// outstanding completes every stage but the last min(ahead, N) issued.
+template <int Q, int N>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (N <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= N) wait_vmcnt<Q * N>();
+    else wait_stages<Q, N - 1>(ahead);
+  }
+}
+
+// Workgroup barrier without a memory fence.  __syncthreads() would first wait
+// for every outstanding vector-memory operation (vmcnt(0)), which includes the
+// direct-to-LDS loads of the stages still in flight; the pipelines below wait
+// for exactly the stage they consume (wait_vmcnt) and then use this barrier.
+// The empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void barrier_no_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+#define MOE_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// global_load_lds_dword[x4]: per-lane global address -> LDS at m0 + 4|16 * lane.
+// The host compilation pass only needs kernel signatures (for the launch
+// stubs); the builtin is kept out of that pass, where clang's deferred
+// diagnostic for it otherwise stops the remaining kernel stubs from being
+// emitted.
+template <int BYTES>
+__device__ __forceinline__ void dma_to_lds(const void* g, void* lds) {
+  static_assert(BYTES == 4 || BYTES == 16, "dword or dwordx4");
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (BYTES == 16)
+    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 4, 0, 0);
+#else
+  (void)g;
+  (void)lds;
+#endif
+}
+
+// Direct global -> LDS loader (global_load_lds_dwordx4) for a tile of ROWS rows
+// x 128 bytes.  One wave instruction writes 1 KiB of LDS = 8 consecutive tile
+// rows, lane l landing at byte 16*l: row r = r0 + l/8, chunk slot l%8.  With
+// the swizzle above that slot holds logical chunk (l%8) ^ swz(r), so lane l
+// loads that chunk of its row; the 8 lanes of a row still cover its 128
+// contiguous bytes.  Wave w issues the instructions for row groups 4*i + w.
+template <int ROWS>
+struct DmaTile {
+  static constexpr int NI = ROWS / 32;  // instructions per wave per K step
+  static_assert(NI >= 1 && ROWS == 32 * NI, "tile rows must be a multiple of 32");
+  const char* src[NI];
+
+  __device__ __forceinline__ static int row_of(int i) { return 8 * (4 * i + wave_id()) + (lane_id() >> 3); }
+  // rowp: address of K-step 0 of tile row row_of(i).
+  __device__ __forceinline__ void set(int i, const char* rowp) {
+    const int l = lane_id();
+    src[i] = rowp + (((l & 7) ^ swz(row_of(i))) << 4);
+  }
+  __device__ __forceinline__ void issue(char* lds, int ks) const {
+    const int w = wave_id();
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (4 * i + w));
+  }
+};
 
 // Global -> register -> LDS loader for a tile of ROWS rows x 128 bytes.
 // Thread t moves chunks (row = t/8 + 32*i, chunk = t%8): eight consecutive

@@ -17,11 +17,11 @@
 
 namespace moe {
 
-template <int BM, int WAVES_M>
+template <int BM, int WAVES_M, int BN = kBN>
 struct Layout {
   static constexpr int WAVES_N = 4 / WAVES_M;
   static constexpr int WTM = BM / WAVES_M;   // tokens per wave
-  static constexpr int WTN = kBN / WAVES_N;  // output features per wave
+  static constexpr int WTN = BN / WAVES_N;   // output features per wave
   static constexpr int NBM = WTM / 32;
   static constexpr int NBN = WTN / 32;
   static_assert(NBM >= 1 && NBN >= 1, "wave tile must hold at least one 32x32 block");
@@ -77,6 +77,9 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const int wave = threadIdx.x >> 6;
   const int wm = wave / L::WAVES_N;
   const int wn = wave % L::WAVES_N;
+  // 32-row token blocks of this wave that hold at least one routed row
+  // (wave-uniform); padding-only blocks skip their LDS reads and MFMAs.
+  const int live = (actual - wm * L::WTM + 31) / 32;
   Acc ag[L::NBN][L::NBM], au[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -94,45 +97,57 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
     gl.issue(st + XB, k);
     ul.issue(st + XB + WB, k);
   };
+  // The K loop is instantiated per count NB of this wave's token blocks that
+  // hold routed rows (chosen once, outside the loop: a branch inside it would
+  // move the accumulators out of AGPRs every step); padding-only blocks get no
+  // LDS reads and no MFMAs.  Every variant issues the same loads and barriers.
+  auto main_loop = [&](auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < nk) issue(s, s);
-  int cur = 0;
-  for (int ks = 0; ks < nk; ++ks) {
-    wait_stages<Q, S - 2>(nk - 1 - ks);
-    barrier_no_fence();
-    if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
-    const char* cx = smem + cur * STAGE;
-    const char* cg = cx + XB;
-    const char* cu = cg + WB;
-    cur = cur + 1 == S ? 0 : cur + 1;
-    // Fragments are double-buffered across the 4 K sub-steps so the LDS reads
-    // of sub-step s+1 are in flight while the MFMAs of sub-step s run.
-    u32x4 xf[2][L::NBM], gf[2][L::NBN], uf[2][L::NBN];
-    auto load_frags = [&](int buf, int s) {
+    for (int s = 0; s < S - 1; ++s)
+      if (s < nk) issue(s, s);
+    int cur = 0;
+    for (int ks = 0; ks < nk; ++ks) {
+      wait_stages<Q, S - 2>(nk - 1 - ks);
+      barrier_no_fence();
+      if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
+      const char* cx = smem + cur * STAGE;
+      const char* cg = cx + XB;
+      const char* cu = cg + WB;
+      cur = cur + 1 == S ? 0 : cur + 1;
+      if constexpr (NB > 0) {
+        // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
+        // sub-step s+1 are in flight while the MFMAs of sub-step s run.
+        u32x4 xf[2][NB], gf[2][L::NBN], uf[2][L::NBN];
+        auto load_frags = [&](int buf, int s) {
 #pragma unroll
-      for (int b = 0; b < L::NBM; ++b) xf[buf][b] = frag(cx, wm * L::WTM + 32 * b, s);
+          for (int b = 0; b < NB; ++b) xf[buf][b] = frag(cx, wm * L::WTM + 32 * b, s);
 #pragma unroll
-      for (int a = 0; a < L::NBN; ++a) {
-        gf[buf][a] = frag(cg, wn * L::WTN + 32 * a, s);
-        uf[buf][a] = frag(cu, wn * L::WTN + 32 * a, s);
-      }
-    };
-    load_frags(0, 0);
+          for (int a = 0; a < L::NBN; ++a) {
+            gf[buf][a] = frag(cg, wn * L::WTN + 32 * a, s);
+            uf[buf][a] = frag(cu, wn * L::WTN + 32 * a, s);
+          }
+        };
+        load_frags(0, 0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int fb = s & 1;
-      if (s < 3) load_frags(fb ^ 1, s + 1);
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+        for (int s = 0; s < 4; ++s) {
+          const int fb = s & 1;
+          if (s < 3) load_frags(fb ^ 1, s + 1);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-      for (int a = 0; a < L::NBN; ++a)
+          for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-        for (int b = 0; b < L::NBM; ++b) {
-          ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
-          au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
+            for (int b = 0; b < NB; ++b) {
+              ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
+              au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
+            }
         }
+      }
     }
-  }
+  };
+  if (live >= L::NBM) main_loop(std::integral_constant<int, L::NBM>{});
+  else if (L::NBM > 1 && live >= 1) main_loop(std::integral_constant<int, 1>{});
+  else main_loop(std::integral_constant<int, 0>{});
   __syncthreads();  // every wave is done with the ring before LDS is reused
 
   const int l = lane_id();
@@ -220,20 +235,20 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   }
 }
 
-template <int BM, int WAVES_M, int S, bool I8, bool FUSED>
+template <int BM, int WAVES_M, int BN, int S, bool I8, bool FUSED>
 __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
-  using L = Layout<BM, WAVES_M>;
+  using L = Layout<BM, WAVES_M, BN>;
   constexpr int XB = BM * kRowBytes;
-  constexpr int WB = kBN * kRowBytes;
+  constexpr int WB = BN * kRowBytes;
   constexpr int STAGE = XB + WB + (I8 ? 1024 : 0);  // int8: + row scales of the step
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
-  const int ntiles = (int)(p.H / kBN);
+  const int ntiles = (int)(p.H / BN);
   Work w;
   if (!schedule(blockIdx.x, p.gpo, p.E, BM, ntiles, p.host_blocks, !FUSED, w)) return;
   const int row0 = w.m_block * BM;
-  const int n0 = w.n_tile * kBN;
+  const int n0 = w.n_tile * BN;
   int actual = 0, gpo_e = 0, go_e = 0;
   const int e = w.e;
   if (e >= 0) {
@@ -246,8 +261,8 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
     if (!FUSED) {
       // Rows owned by no valid token are written as 0 (problem_detail.json:50 note 4).
       _Float16* o = reinterpret_cast<_Float16*>(p.out);
-      for (int idx = threadIdx.x; idx < BM * (kBN / 8); idx += kThreads) {
-        const int r = idx / (kBN / 8), c = idx % (kBN / 8);
+      for (int idx = threadIdx.x; idx < BM * (BN / 8); idx += kThreads) {
+        const int r = idx / (BN / 8), c = idx % (BN / 8);
         *reinterpret_cast<u32x4*>(o + (int64_t)(row0 + r) * p.H + n0 + 8 * c) = u32x4{0, 0, 0, 0};
       }
     }
@@ -257,18 +272,19 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
   DmaTile<BM> al;
-  DmaTile<kBN> wl;
+  DmaTile<BN> wl;
 #pragma unroll
   for (int i = 0; i < DmaTile<BM>::NI; ++i)
     al.set(i, p.a + (int64_t)(row0 + DmaTile<BM>::row_of(i)) * kbytes);
   const char* wbase = p.wd + ((int64_t)e * p.H + n0) * kbytes;
 #pragma unroll
-  for (int i = 0; i < DmaTile<kBN>::NI; ++i) wl.set(i, wbase + DmaTile<kBN>::row_of(i) * kbytes);
+  for (int i = 0; i < DmaTile<BN>::NI; ++i) wl.set(i, wbase + DmaTile<BN>::row_of(i) * kbytes);
 
   const int wave = threadIdx.x >> 6;
   const int wm = wave / L::WAVES_N;
   const int wn = wave % L::WAVES_N;
   const int l = lane_id();
+  const int live = (actual - wm * L::WTM + 31) / 32;  // see Stage 1
   f32x16 acc[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -283,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
     const int r = 64 * wave_id() + l;
     scale_src = p.a_scale + row0 + (r < BM ? r : 0);
   }
-  constexpr int Q = DmaTile<BM>::NI + DmaTile<kBN>::NI + (I8 ? 1 : 0);
+  constexpr int Q = DmaTile<BM>::NI + DmaTile<BN>::NI + (I8 ? 1 : 0);
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
     al.issue(st, k);
@@ -291,70 +307,77 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
     if constexpr (I8)
       dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + XB + WB + 256 * wave_id());
   };
+  // K loop instantiated per count of live token blocks (see Stage 1).
+  auto main_loop = [&](auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < nk) issue(s, s);
-  int cur = 0;
-  for (int ks = 0; ks < nk; ++ks) {
-    wait_stages<Q, S - 2>(nk - 1 - ks);
-    barrier_no_fence();
-    if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
-    const char* ca = smem + cur * STAGE;
-    const char* cw = ca + XB;
-    cur = cur + 1 == S ? 0 : cur + 1;
-    // Fragments double-buffered across the K sub-steps (see Stage 1).
-    u32x4 af[2][L::NBM], wf[2][L::NBN];
-    auto load_frags = [&](int buf, int s) {
+    for (int s = 0; s < S - 1; ++s)
+      if (s < nk) issue(s, s);
+    int cur = 0;
+    for (int ks = 0; ks < nk; ++ks) {
+      wait_stages<Q, S - 2>(nk - 1 - ks);
+      barrier_no_fence();
+      if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
+      const char* ca = smem + cur * STAGE;
+      const char* cw = ca + XB;
+      cur = cur + 1 == S ? 0 : cur + 1;
+      if constexpr (NB > 0) {
+        u32x4 af[2][NB], wf[2][L::NBN];
+        auto load_frags = [&](int buf, int s) {
 #pragma unroll
-      for (int b = 0; b < L::NBM; ++b) af[buf][b] = frag(ca, wm * L::WTM + 32 * b, s);
+          for (int b = 0; b < NB; ++b) af[buf][b] = frag(ca, wm * L::WTM + 32 * b, s);
 #pragma unroll
-      for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(cw, wn * L::WTN + 32 * a, s);
-    };
-    if constexpr (!I8) {
-      load_frags(0, 0);
+          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(cw, wn * L::WTN + 32 * a, s);
+        };
+        if constexpr (!I8) {
+          load_frags(0, 0);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int fb = s & 1;
-        if (s < 3) load_frags(fb ^ 1, s + 1);
-        __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+          for (int s = 0; s < 4; ++s) {
+            const int fb = s & 1;
+            if (s < 3) load_frags(fb ^ 1, s + 1);
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-        for (int a = 0; a < L::NBN; ++a)
+            for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-          for (int b = 0; b < L::NBM; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
+              for (int b = 0; b < NB; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
+          }
+        } else {
+          // One K step of int8 is one 128-column scale block of the
+          // intermediate: exact int32 partial product, then
+          // acc += partial * s_h[row, block].
+          const float* scl = reinterpret_cast<const float*>(cw + WB);
+          float sc[NB];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) sc[b] = scl[wm * L::WTM + 32 * b + (l & 31)];
+          i32x16 ia[L::NBN][NB];
+#pragma unroll
+          for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) ia[a][b] = i32x16{};
+          load_frags(0, 0);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int fb = s & 1;
+            if (s < 3) load_frags(fb ^ 1, s + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+              for (int b = 0; b < NB; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
+          }
+#pragma unroll
+          for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
+        }
       }
-    } else {
-      // One K step of int8 is one 128-column scale block of the intermediate:
-      // exact int32 partial product, then acc += partial * s_h[row, block].
-      const float* scl = reinterpret_cast<const float*>(cw + WB);
-      float sc[L::NBM];
-#pragma unroll
-      for (int b = 0; b < L::NBM; ++b) sc[b] = scl[wm * L::WTM + 32 * b + (l & 31)];
-      i32x16 ia[L::NBN][L::NBM];
-#pragma unroll
-      for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-        for (int b = 0; b < L::NBM; ++b) ia[a][b] = i32x16{};
-      load_frags(0, 0);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int fb = s & 1;
-        if (s < 3) load_frags(fb ^ 1, s + 1);
-        __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
-#pragma unroll
-        for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-          for (int b = 0; b < L::NBM; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
-      }
-#pragma unroll
-      for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-        for (int b = 0; b < L::NBM; ++b)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
     }
-  }
+  };
+  if (live >= L::NBM) main_loop(std::integral_constant<int, L::NBM>{});
+  else if (L::NBM > 1 && live >= 1) main_loop(std::integral_constant<int, 1>{});
+  else main_loop(std::integral_constant<int, 0>{});
 
   _Float16* o = reinterpret_cast<_Float16*>(p.out);
 #pragma unroll
@@ -414,7 +437,10 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
 #define MOE_S1_STAGES_32 4
 #endif
 #ifndef MOE_S2_STAGES_128
-#define MOE_S2_STAGES_128 2
+#define MOE_S2_STAGES_128 3
+#endif
+#ifndef MOE_S2_BN_128
+#define MOE_S2_BN_128 256
 #endif
 #ifndef MOE_S2_STAGES_64
 #define MOE_S2_STAGES_64 4
@@ -436,12 +462,23 @@ static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
                      0, s, p);
   return hipGetLastError();
 }
-template <int BM, int WM, bool I8, bool FUSED>
-static hipError_t go2(const Stage2Params& p, int64_t grid, hipStream_t s) {
+// Stage 2's K loop is short (I / 64 steps), so its wide-M tiles take a
+// 256-wide N tile when H allows: half the workgroups, half the re-reads of the
+// intermediate, and twice the work behind each workgroup's pipeline fill and
+// epilogue.
+template <int BM, int WM, int BN, bool I8, bool FUSED>
+static hipError_t go2(const Stage2Params& p, int64_t max_blocks, hipStream_t s) {
   constexpr int kS = s2_stages(BM);
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, kS, I8, FUSED>), dim3((unsigned)grid), dim3(kThreads),
+  const int64_t grid = schedule_grid(max_blocks, p.H / BN);
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, I8, FUSED>), dim3((unsigned)grid), dim3(kThreads),
                      0, s, p);
   return hipGetLastError();
+}
+template <bool I8, bool FUSED>
+static hipError_t go2_128(const Stage2Params& p, int64_t mb, hipStream_t s) {
+  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, I8, FUSED>(p, mb, s);
+  return go2<128, 2, 128, I8, FUSED>(p, mb, s);
 }
 
 hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, bool gather,
@@ -466,16 +503,15 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, bool int8, boo
                          int64_t max_blocks, hipStream_t s) {
   Stage2Params p = params;
   p.host_blocks = (int)max_blocks;
-  const int64_t grid = schedule_grid(max_blocks, p.H / kBN);
-  if (grid <= 0) return hipSuccess;
+  const int64_t mb = max_blocks;
   if (!fused) {
-    if (block_m == 128 && !int8) return go2<128, 2, false, false>(p, grid, s);
+    if (block_m == 128 && !int8) return go2_128<false, false>(p, mb, s);
     return hipErrorInvalidValue;
   }
   switch (block_m) {
-    case 32: return int8 ? go2<32, 1, true, true>(p, grid, s) : go2<32, 1, false, true>(p, grid, s);
-    case 64: return int8 ? go2<64, 1, true, true>(p, grid, s) : go2<64, 1, false, true>(p, grid, s);
-    case 128: return int8 ? go2<128, 2, true, true>(p, grid, s) : go2<128, 2, false, true>(p, grid, s);
+    case 32: return int8 ? go2<32, 1, kBN, true, true>(p, mb, s) : go2<32, 1, kBN, false, true>(p, mb, s);
+    case 64: return int8 ? go2<64, 1, kBN, true, true>(p, mb, s) : go2<64, 1, kBN, false, true>(p, mb, s);
+    case 128: return int8 ? go2_128<true, true>(p, mb, s) : go2_128<false, true>(p, mb, s);
   }
   return hipErrorInvalidValue;
 }

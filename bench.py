@@ -123,6 +123,22 @@ def cpu_baseline(inp, ids_np, budget_s=15.0):
                         f"os.cpu_count()={os.cpu_count()}"))
 
 
+def recorded_traffic(config, kernel_prefix):
+    """HBM bytes per dispatch of the given kernel from the committed counter
+    summary profiles/traffic_<config>.json (two rocprofv3 --pmc passes,
+    FETCH_SIZE then WRITE_SIZE, calibrated on a plain 1 GiB copy; the command
+    lines are in profiles/traffic_<config>.md).  None when absent."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    for name, k in rec.get("kernels", {}).items():
+        if name.startswith(kernel_prefix):
+            return dict(bytes=k["hbm_bytes"], kernel=name, source=f"profiles/traffic_{config}.md")
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -213,6 +229,7 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = op_bytes / (ms * 1e-3) / 1e9
     ideal_ms = max(flops / (PEAK_F16_TFLOPS * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
+    s1_traffic = recorded_traffic(args.config, "moe::stage1_kernel")
 
     check_res = None
     if not args.no_check:
@@ -279,7 +296,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(s1_bytes / (s1_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": None if s1_traffic is None else s1_traffic["bytes"],
+            "traffic_source": None if s1_traffic is None else s1_traffic["source"],
             "algorithmic_bytes": int(s1_bytes),
             "mfma_tflops": round(s1_flops / (s1_ms * 1e-3) / 1e12, 2),
         },

@@ -17,9 +17,9 @@
 
 namespace moe {
 
-template <int BM, int WAVES_M, int BN = kBN>
+template <int BM, int WAVES_M, int BN, int NW>
 struct Layout {
-  static constexpr int WAVES_N = 4 / WAVES_M;
+  static constexpr int WAVES_N = NW / WAVES_M;
   static constexpr int WTM = BM / WAVES_M;   // tokens per wave
   static constexpr int WTN = BN / WAVES_N;   // output features per wave
   static constexpr int NBM = WTM / 32;
@@ -27,9 +27,9 @@ struct Layout {
   static_assert(NBM >= 1 && NBN >= 1, "wave tile must hold at least one 32x32 block");
 };
 
-template <int BM, int WAVES_M, int S, bool I8, bool GATHER>
-__global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
-  using L = Layout<BM, WAVES_M>;
+template <int BM, int WAVES_M, int S, int NW, bool I8, bool GATHER>
+__global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
+  using L = Layout<BM, WAVES_M, kBN, NW>;
   using Acc = typename std::conditional<I8, i32x16, f32x16>::type;
   constexpr int XB = BM * kRowBytes;
   constexpr int WB = kBN * kRowBytes;
@@ -51,11 +51,11 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
 
-  DmaTile<BM> xl;
-  DmaTile<kBN> gl, ul;
+  DmaTile<BM, NW> xl;
+  DmaTile<kBN, NW> gl, ul;
 #pragma unroll
-  for (int i = 0; i < DmaTile<BM>::NI; ++i) {
-    const int r = DmaTile<BM>::row_of(i);
+  for (int i = 0; i < DmaTile<BM, NW>::NI; ++i) {
+    const int r = DmaTile<BM, NW>::row_of(i);
     int64_t src_row;
     if (GATHER) {
       const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
@@ -68,8 +68,8 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const char* gbase = p.wg + ((int64_t)e * p.I + n0) * kbytes;
   const char* ubase = p.wu + ((int64_t)e * p.I + n0) * kbytes;
 #pragma unroll
-  for (int i = 0; i < DmaTile<kBN>::NI; ++i) {
-    const int r = DmaTile<kBN>::row_of(i);
+  for (int i = 0; i < DmaTile<kBN, NW>::NI; ++i) {
+    const int r = DmaTile<kBN, NW>::row_of(i);
     gl.set(i, gbase + r * kbytes);
     ul.set(i, ubase + r * kbytes);
   }
@@ -79,6 +79,9 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   const int wn = wave % L::WAVES_N;
   // 32-row token blocks of this wave that hold at least one routed row
   // (wave-uniform); padding-only blocks skip their LDS reads and MFMAs.
+  // (Skipping costs L2 sharing between the M blocks of one expert -- a block
+  // with less MFMA work runs ahead of its siblings -- but measured faster
+  // overall than keeping siblings in step.)
   const int live = (actual - wm * L::WTM + 31) / 32;
   Acc ag[L::NBN][L::NBM], au[L::NBN][L::NBM];
 #pragma unroll
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
     }
 
   // S-stage ring: stages ks+1 .. ks+S-2 stay in flight while stage ks is used.
-  constexpr int Q = DmaTile<BM>::NI + 2 * DmaTile<kBN>::NI;  // loads per wave per stage
+  constexpr int Q = DmaTile<BM, NW>::NI + 2 * DmaTile<kBN, NW>::NI;  // loads per wave per stage
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
     xl.issue(st, k);
@@ -235,12 +238,12 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Params p) {
   }
 }
 
-template <int BM, int WAVES_M, int BN, int S, bool I8, bool FUSED>
-__global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
-  using L = Layout<BM, WAVES_M, BN>;
+template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED>
+__global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
+  using L = Layout<BM, WAVES_M, BN, NW>;
   constexpr int XB = BM * kRowBytes;
   constexpr int WB = BN * kRowBytes;
-  constexpr int STAGE = XB + WB + (I8 ? 1024 : 0);  // int8: + row scales of the step
+  constexpr int STAGE = XB + WB + (I8 ? 256 * NW : 0);  // int8: + row scales of the step
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
     if (!FUSED) {
       // Rows owned by no valid token are written as 0 (problem_detail.json:50 note 4).
       _Float16* o = reinterpret_cast<_Float16*>(p.out);
-      for (int idx = threadIdx.x; idx < BM * (BN / 8); idx += kThreads) {
+      for (int idx = threadIdx.x; idx < BM * (BN / 8); idx += 64 * NW) {
         const int r = idx / (BN / 8), c = idx % (BN / 8);
         *reinterpret_cast<u32x4*>(o + (int64_t)(row0 + r) * p.H + n0 + 8 * c) = u32x4{0, 0, 0, 0};
       }
@@ -271,14 +274,14 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
 
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
-  DmaTile<BM> al;
-  DmaTile<BN> wl;
+  DmaTile<BM, NW> al;
+  DmaTile<BN, NW> wl;
 #pragma unroll
-  for (int i = 0; i < DmaTile<BM>::NI; ++i)
-    al.set(i, p.a + (int64_t)(row0 + DmaTile<BM>::row_of(i)) * kbytes);
+  for (int i = 0; i < DmaTile<BM, NW>::NI; ++i)
+    al.set(i, p.a + (int64_t)(row0 + DmaTile<BM, NW>::row_of(i)) * kbytes);
   const char* wbase = p.wd + ((int64_t)e * p.H + n0) * kbytes;
 #pragma unroll
-  for (int i = 0; i < DmaTile<BN>::NI; ++i) wl.set(i, wbase + DmaTile<BN>::row_of(i) * kbytes);
+  for (int i = 0; i < DmaTile<BN, NW>::NI; ++i) wl.set(i, wbase + DmaTile<BN, NW>::row_of(i) * kbytes);
 
   const int wave = threadIdx.x >> 6;
   const int wm = wave / L::WAVES_N;
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void stage2_kernel(Stage2Params p) {
     const int r = 64 * wave_id() + l;
     scale_src = p.a_scale + row0 + (r < BM ? r : 0);
   }
-  constexpr int Q = DmaTile<BM>::NI + DmaTile<BN>::NI + (I8 ? 1 : 0);
+  constexpr int Q = DmaTile<BM, NW>::NI + DmaTile<BN, NW>::NI + (I8 ? 1 : 0);
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
     al.issue(st, k);
@@ -455,30 +458,41 @@ constexpr int s2_stages(int bm) {
   return bm == 128 ? MOE_S2_STAGES_128 : (bm == 64 ? MOE_S2_STAGES_64 : MOE_S2_STAGES_32);
 }
 
-template <int BM, int WM, bool I8, bool GATHER>
+// Waves per workgroup of the 128-row tiles (4 = one wave per SIMD; 8 = two,
+// so one wave's LDS / barrier latency hides behind the other's MFMAs).
+#ifndef MOE_S1_WAVES_128
+#define MOE_S1_WAVES_128 8
+#endif
+#ifndef MOE_S2_WAVES_128
+#define MOE_S2_WAVES_128 8
+#endif
+
+template <int BM, int WM, int NW, bool I8, bool GATHER>
 static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
   constexpr int kS = s1_stages(BM);
-  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, I8, GATHER>), dim3((unsigned)grid), dim3(kThreads),
-                     0, s, p);
+  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, NW, I8, GATHER>), dim3((unsigned)grid),
+                     dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
+
 // Stage 2's K loop is short (I / 64 steps), so its wide-M tiles take a
 // 256-wide N tile when H allows: half the workgroups, half the re-reads of the
 // intermediate, and twice the work behind each workgroup's pipeline fill and
 // epilogue.
-template <int BM, int WM, int BN, bool I8, bool FUSED>
+template <int BM, int WM, int BN, int NW, bool I8, bool FUSED>
 static hipError_t go2(const Stage2Params& p, int64_t max_blocks, hipStream_t s) {
   constexpr int kS = s2_stages(BM);
   const int64_t grid = schedule_grid(max_blocks, p.H / BN);
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, I8, FUSED>), dim3((unsigned)grid), dim3(kThreads),
-                     0, s, p);
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED>), dim3((unsigned)grid),
+                     dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
 template <bool I8, bool FUSED>
 static hipError_t go2_128(const Stage2Params& p, int64_t mb, hipStream_t s) {
-  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, I8, FUSED>(p, mb, s);
-  return go2<128, 2, 128, I8, FUSED>(p, mb, s);
+  constexpr int NW = MOE_S2_WAVES_128;
+  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, NW, I8, FUSED>(p, mb, s);
+  return go2<128, 2, 128, NW, I8, FUSED>(p, mb, s);
 }
 
 hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, bool gather,
@@ -487,14 +501,15 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, boo
   p.host_blocks = (int)max_blocks;
   const int64_t grid = schedule_grid(max_blocks, p.I / kBN);
   if (grid <= 0) return hipSuccess;
+  constexpr int NW = MOE_S1_WAVES_128;
   if (!gather) {
-    if (block_m == 128 && !int8) return go1<128, 2, false, false>(p, grid, s);
+    if (block_m == 128 && !int8) return go1<128, 2, NW, false, false>(p, grid, s);
     return hipErrorInvalidValue;
   }
   switch (block_m) {
-    case 32: return int8 ? go1<32, 1, true, true>(p, grid, s) : go1<32, 1, false, true>(p, grid, s);
-    case 64: return int8 ? go1<64, 1, true, true>(p, grid, s) : go1<64, 1, false, true>(p, grid, s);
-    case 128: return int8 ? go1<128, 2, true, true>(p, grid, s) : go1<128, 2, false, true>(p, grid, s);
+    case 32: return int8 ? go1<32, 1, 4, true, true>(p, grid, s) : go1<32, 1, 4, false, true>(p, grid, s);
+    case 64: return int8 ? go1<64, 1, 4, true, true>(p, grid, s) : go1<64, 1, 4, false, true>(p, grid, s);
+    case 128: return int8 ? go1<128, 2, NW, true, true>(p, grid, s) : go1<128, 2, NW, false, true>(p, grid, s);
   }
   return hipErrorInvalidValue;
 }
@@ -509,8 +524,8 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, bool int8, boo
     return hipErrorInvalidValue;
   }
   switch (block_m) {
-    case 32: return int8 ? go2<32, 1, kBN, true, true>(p, mb, s) : go2<32, 1, kBN, false, true>(p, mb, s);
-    case 64: return int8 ? go2<64, 1, kBN, true, true>(p, mb, s) : go2<64, 1, kBN, false, true>(p, mb, s);
+    case 32: return int8 ? go2<32, 1, kBN, 4, true, true>(p, mb, s) : go2<32, 1, kBN, 4, false, true>(p, mb, s);
+    case 64: return int8 ? go2<64, 1, kBN, 4, true, true>(p, mb, s) : go2<64, 1, kBN, 4, false, true>(p, mb, s);
     case 128: return int8 ? go2_128<true, true>(p, mb, s) : go2_128<false, true>(p, mb, s);
   }
   return hipErrorInvalidValue;

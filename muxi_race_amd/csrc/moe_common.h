@@ -31,7 +31,6 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;      // 4 waves per workgroup
 constexpr int kRowBytes = 128;     // bytes of one tile row per K step
 constexpr int kBN = 128;           // output-feature tile (N) of every GEMM
 constexpr int kNumXcd = 8;         // MI355X: 8 XCDs, workgroups dealt round-robin
@@ -108,18 +107,19 @@ __device__ __forceinline__ void dma_to_lds(const void* g, void* lds) {
 }
 
 // Direct global -> LDS loader (global_load_lds_dwordx4) for a tile of ROWS rows
-// x 128 bytes.  One wave instruction writes 1 KiB of LDS = 8 consecutive tile
-// rows, lane l landing at byte 16*l: row r = r0 + l/8, chunk slot l%8.  With
-// the swizzle above that slot holds logical chunk (l%8) ^ swz(r), so lane l
-// loads that chunk of its row; the 8 lanes of a row still cover its 128
-// contiguous bytes.  Wave w issues the instructions for row groups 4*i + w.
-template <int ROWS>
+// x 128 bytes, issued by the NW waves of a workgroup.  One wave instruction
+// writes 1 KiB of LDS = 8 consecutive tile rows, lane l landing at byte 16*l:
+// row r = r0 + l/8, chunk slot l%8.  With the swizzle above that slot holds
+// logical chunk (l%8) ^ swz(r), so lane l loads that chunk of its row; the 8
+// lanes of a row still cover its 128 contiguous bytes.  Wave w issues the
+// instructions for row groups NW*i + w.
+template <int ROWS, int NW>
 struct DmaTile {
-  static constexpr int NI = ROWS / 32;  // instructions per wave per K step
-  static_assert(NI >= 1 && ROWS == 32 * NI, "tile rows must be a multiple of 32");
+  static constexpr int NI = ROWS / (8 * NW);  // instructions per wave per K step
+  static_assert(NI >= 1 && ROWS == 8 * NW * NI, "tile rows must be a multiple of 8 * waves");
   const char* src[NI];
 
-  __device__ __forceinline__ static int row_of(int i) { return 8 * (4 * i + wave_id()) + (lane_id() >> 3); }
+  __device__ __forceinline__ static int row_of(int i) { return 8 * (NW * i + wave_id()) + (lane_id() >> 3); }
   // rowp: address of K-step 0 of tile row row_of(i).
   __device__ __forceinline__ void set(int i, const char* rowp) {
     const int l = lane_id();
@@ -129,38 +129,7 @@ struct DmaTile {
     const int w = wave_id();
 #pragma unroll
     for (int i = 0; i < NI; ++i)
-      dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (4 * i + w));
-  }
-};
-
-// Global -> register -> LDS loader for a tile of ROWS rows x 128 bytes.
-// Thread t moves chunks (row = t/8 + 32*i, chunk = t%8): eight consecutive
-// lanes cover one 128-byte row segment, so every wave load is 8 fully used
-// 128-byte lines.
-template <int ROWS>
-struct TileLoader {
-  static constexpr int CH = ROWS * 8 / kThreads;
-  static_assert(CH >= 1 && ROWS * 8 == CH * kThreads, "tile rows must be a multiple of 32");
-  const char* src[CH];
-  int dst[CH];
-  u32x4 reg[CH];
-
-  __device__ __forceinline__ static int row_of(int i) { return (threadIdx.x >> 3) + 32 * i; }
-
-  // rowp: address of K-step 0 of tile row row_of(i).
-  __device__ __forceinline__ void set(int i, const char* rowp) {
-    const int c = threadIdx.x & 7;
-    src[i] = rowp + (c << 4);
-    dst[i] = lds_swz(row_of(i), c);
-  }
-  __device__ __forceinline__ void load(int ks) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i)
-      reg[i] = *reinterpret_cast<const u32x4*>(src[i] + (size_t)ks * kRowBytes);
-  }
-  __device__ __forceinline__ void store(char* lds) const {
-#pragma unroll
-    for (int i = 0; i < CH; ++i) *reinterpret_cast<u32x4*>(lds + dst[i]) = reg[i];
+      dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
   }
 };
 
@@ -216,6 +185,7 @@ struct Work {
   int e;        // expert, or -1 for a tail block owned by no expert
   int n_tile;
   int m_block;
+  int blocks;   // M blocks of expert e (workgroups sharing this weight tile)
 };
 
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM,
@@ -234,6 +204,7 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
     w.e = -1;
     w.m_block = expert_blocks + t / ntiles;
     w.n_tile = t % ntiles;
+    w.blocks = 1;
     return true;
   }
   // e = (number of experts whose first item is <= v) - 1, found with ballots.
@@ -254,6 +225,7 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
   w.e = e;
   w.n_tile = local / mb;
   w.m_block = b0 + local % mb;
+  w.blocks = mb;
   return w.m_block >= 0 && w.m_block < host_blocks && w.n_tile < ntiles;
 }
 

@@ -148,6 +148,8 @@ def main():
     ap.add_argument("--block-m", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the sampled oracle check")
+    ap.add_argument("--w8a8", action="store_true", help="run the int8 path (default for --config w8a8)")
+    ap.add_argument("--fp16", action="store_true", help="run the fp16 path even for --config w8a8")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -166,25 +168,41 @@ def main():
     torch.cuda.set_device(dev)
     inp = make_inputs(args.config, dev)
     T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
+    w8 = (args.config == "w8a8" or args.w8a8) and not args.fp16
     L = lib()
     bm = args.block_m or int(L.moe_pick_block_m(T, E, k))
-    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, 0)
+    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, int(w8))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
     ids = torch.empty((T, k), dtype=torch.int32, device=dev)
     wts = torch.empty((T, k), dtype=torch.float32, device=dev)
     P = ctypes.c_void_p
     stream = P(torch.cuda.current_stream(dev).cuda_stream)
-    cargs = [P(inp["x"].data_ptr()), P(inp["logits"].data_ptr()),
-             P(0 if inp["bias"] is None else inp["bias"].data_ptr()), P(inp["wg"].data_ptr()),
-             P(inp["wu"].data_ptr()), P(inp["wd"].data_ptr()), P(out.data_ptr()), T, H, I, E, k, bm,
-             P(ws.data_ptr()), ws.numel(), P(ids.data_ptr()), P(wts.data_ptr()), stream]
+    head = [P(inp["x"].data_ptr()), P(inp["logits"].data_ptr()),
+            P(0 if inp["bias"] is None else inp["bias"].data_ptr())]
+    tail = [P(out.data_ptr()), T, H, I, E, k, bm, P(ws.data_ptr()), ws.numel(), P(ids.data_ptr()),
+            P(wts.data_ptr()), stream]
+    quant_ms = None
+    if w8:
+        # weights are quantised once, outside the timed step (they are static)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        qw = m.quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"])
+        b.record()
+        torch.cuda.synchronize()
+        quant_ms = a.elapsed_time(b)
+        cargs = head + [P(t.data_ptr()) for t in (qw.q_gate, qw.s_gate, qw.q_up, qw.s_up, qw.q_down,
+                                                   qw.s_down)] + tail
+        fwd, fwd_ev, name = L.moe_fused_forward_w8a8, L.moe_fused_forward_w8a8_events, "moe_fused_forward_w8a8"
+    else:
+        cargs = head + [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + tail
+        fwd, fwd_ev, name = L.moe_fused_forward, L.moe_fused_forward_events, "moe_fused_forward"
 
     def step(events=None):
         if events is None:
-            check(L.moe_fused_forward(*cargs), "moe_fused_forward")
+            check(fwd(*cargs), name)
         else:
-            check(L.moe_fused_forward_events(*cargs, events), "moe_fused_forward_events")
+            check(fwd_ev(*cargs, events), name + "_events")
 
     for _ in range(args.warmup):
         step()
@@ -217,34 +235,49 @@ def main():
     hev.close()
     stage_ms = {n: round(statistics.mean(v), 4) for n, v in stage.items()}
 
-    # algorithmic work
+    # algorithmic work: routed pairs only (padding excluded); weights of the
+    # experts actually touched, read once; activations, logits, routing
     ids_np = ids.cpu().numpy()
     touched = np.unique(ids_np).size
     Pn = T * k
+    bw = 1 if w8 else 2
     flops = 6.0 * H * I * Pn
-    op_bytes = touched * 3.0 * H * I * 2 + 2.0 * T * H * 2 + T * E * 4 + Pn * 8
-    s1_bytes = touched * 2.0 * H * I * 2 + T * H * 2 + Pn * I * 2
+    scale_bytes = touched * (2.0 * I + H) * 4 if w8 else 0.0
+    op_bytes = touched * 3.0 * H * I * bw + scale_bytes + 2.0 * T * H * 2 + T * E * 4 + Pn * 8
+    s1_bytes = touched * 2.0 * H * I * bw + T * H * bw + Pn * I * bw
     s1_flops = 4.0 * H * I * Pn
     s1_ms = stage_ms["stage1"]
+    peak_c = PEAK_I8_TOPS if w8 else PEAK_F16_TFLOPS
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = op_bytes / (ms * 1e-3) / 1e9
-    ideal_ms = max(flops / (PEAK_F16_TFLOPS * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
-    s1_traffic = recorded_traffic(args.config, "moe::stage1_kernel")
+    ideal_ms = max(flops / (peak_c * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
+    s1_hbm_bound = s1_bytes / (PEAK_HBM_GBS * 1e9) >= s1_flops / (peak_c * 1e12)
+    s1_traffic = recorded_traffic(args.config + ("_w8a8" if w8 and args.config != "w8a8" else ""),
+                                  "moe::stage1_kernel")
 
     check_res = None
     if not args.no_check:
-        from oracle import fused_moe_forward, route_topk
+        from oracle import fused_moe_forward, route_topk, w8a8_forward
         rid, _ = route_topk(inp["logits"].cpu().numpy(), k,
                             None if inp["bias"] is None else inp["bias"].cpu().numpy())
         ids_ok = bool(np.array_equal(ids_np, rid))
         rows = np.sort(np.random.default_rng(0).choice(T, min(T, 4), replace=False))
         r = torch.from_numpy(rows).to(dev)
-        ref = fused_moe_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), inp["wg"], inp["wu"],
-                                inp["wd"], k, None if inp["bias"] is None else inp["bias"].cpu()).float()
+        bias_c = None if inp["bias"] is None else inp["bias"].cpu()
+        ref16 = fused_moe_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), inp["wg"], inp["wu"],
+                                  inp["wd"], k, bias_c).float()
         got = out[r].float().cpu()
-        ok = bool(torch.isfinite(got).all()) and bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
-        check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
-                     "within_rtol2e-2_atol1e-2": ok}
+        tol = lambda ref: bool(torch.isfinite(got).all()) and bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
+        if w8:
+            ref8 = w8a8_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), qw.q_gate.cpu().numpy(),
+                                qw.s_gate.cpu().numpy(), qw.q_up.cpu().numpy(), qw.s_up.cpu().numpy(),
+                                qw.q_down.cpu().numpy(), qw.s_down.cpu().numpy(), k, bias_c).float()
+            check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
+                         "w8a8_oracle_within_rtol2e-2_atol1e-2": tol(ref8),
+                         "rel_l2_vs_fp16_oracle": round(float((got - ref16).norm() / ref16.norm()), 5)}
+        else:
+            check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
+                         "within_rtol2e-2_atol1e-2": tol(ref16)}
 
     cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
 
@@ -267,7 +300,7 @@ def main():
     res = {
         "metric": METRIC,
         "value": round(tflops, 3),
-        "unit": "TFLOP/s",
+        "unit": "TOP/s" if w8 else "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -276,29 +309,33 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": "int8" if w8 else "fp16",
         "data": "synthetic (seeded: x~N(0,1), weights~N(0,0.02), logits~N(0,1)"
                 + (", bias~N(0,0.5)" if CONFIGS[args.config][5] == "normal" else "")
                 + (", bias=-1.2*ln(rank+1)" if CONFIGS[args.config][5] == "zipf" else "") + ")",
-        "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} fp16",
+        "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} "
+                               + ("W8A8 int8" if w8 else "fp16"),
                    "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
                    "block_m": bm, "experts_touched": int(touched)},
         "gb_per_s": round(gbs, 1),
-        "frac_mfma_peak": round(tflops / PEAK_F16_TFLOPS, 4),
+        "frac_mfma_peak": round(tflops / peak_c, 4),
         "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
         "roofline_ideal_ms": round(ideal_ms, 4),
         "frac_of_roofline_time": round(ideal_ms / ms, 4),
         "stage_ms": stage_ms,
         "roofline": {
             "kernel": "stage1 (gathered gate/up GEMM + SiLU*up)",
-            "bound": "hbm",
-            "achieved": round(s1_bytes / (s1_ms * 1e-3) / 1e9, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(s1_bytes / (s1_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "bound": "hbm" if s1_hbm_bound else "mfma",
+            "achieved": round(s1_bytes / (s1_ms * 1e-3) / 1e9, 1) if s1_hbm_bound
+            else round(s1_flops / (s1_ms * 1e-3) / 1e12, 2),
+            "peak": PEAK_HBM_GBS if s1_hbm_bound else peak_c,
+            "unit": "GB/s" if s1_hbm_bound else ("TOP/s" if w8 else "TFLOP/s"),
+            "frac": round(s1_bytes / (s1_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if s1_hbm_bound
+            else round(s1_flops / (s1_ms * 1e-3) / 1e12 / peak_c, 4),
             "traffic": None if s1_traffic is None else s1_traffic["bytes"],
             "traffic_source": None if s1_traffic is None else s1_traffic["source"],
             "algorithmic_bytes": int(s1_bytes),
+            "algorithmic_flops": int(s1_flops),
             "mfma_tflops": round(s1_flops / (s1_ms * 1e-3) / 1e12, 2),
         },
         "cpu_baseline": cpu,
@@ -307,6 +344,8 @@ def main():
     }
     if copy_gbs is not None:
         res["calib_copy_gb_per_s"] = copy_gbs
+    if quant_ms is not None:
+        res["weight_quantisation_ms_once"] = round(quant_ms, 3)
     print(json.dumps(res), flush=True)
 
 

@@ -38,6 +38,8 @@ SIGNATURES = {
     "moe_quantize_rows_w8": (_int, [_p, _i64, _i64, _p, _p, _p]),
     "moe_fused_forward_w8a8": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
+    "moe_fused_forward_w8a8_events": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                                             _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p]),
 }
 
 _LIB = None

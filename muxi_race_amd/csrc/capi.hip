@@ -298,4 +298,16 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                       topk_weights_out, stream, nullptr);
 }
 
+int moe_fused_forward_w8a8_events(const void* x, const float* logits, const float* bias,
+                                  const int8_t* wq_gate, const float* s_gate, const int8_t* wq_up,
+                                  const float* s_up, const int8_t* wq_down, const float* s_down,
+                                  void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                  int64_t block_m, void* workspace, int64_t workspace_bytes,
+                                  int32_t* topk_ids_out, float* topk_weights_out, void* stream,
+                                  void* const* stage_events) {
+  return fused_common(true, x, logits, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+                      T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
+                      topk_weights_out, stream, stage_events);
+}
+
 }  // extern "C"

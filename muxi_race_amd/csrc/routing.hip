@@ -108,45 +108,84 @@ hipError_t launch_route_topk(const float* logits, const float* bias, int T, int 
 }
 
 // ---------------------------------------------------------------------------
-// moe_align: one workgroup of 1024 threads (16 waves).
-//   1. LDS histogram of expert ids (order-free counts).
-//   2. Wave 0 scans counts -> group_offsets, padded counts -> padded offsets.
-//   3. Pairs are placed in chunks of 1024 in pair order.  Inside a wave, lanes
-//      holding the same expert are found by ANDing ballots of the expert-id
-//      bits; a lane's slot = expert cursor + same-expert pairs of earlier waves
-//      in the chunk + same-expert lanes below it.  Placement therefore follows
-//      pair order exactly, independent of timing.
-//   4. Sentinel rows and the block -> expert map.
+// moe_align: one workgroup of NW waves; wave w owns the contiguous pair range
+// [w*R, (w+1)*R).  Ranks come from ballots: the lanes of a wave that hold the
+// same expert are found by ANDing ballots of the expert-id bits, and a lane's
+// rank is the number of such lanes below it.  No barrier inside the walks and
+// no atomics, so placement follows pair order exactly:
+//   1. count:  each wave builds its private per-expert histogram hist[w][e];
+//   2. scan:   hist[w][e] becomes the wave's first row for expert e
+//              (padded expert offset + counts of the waves before it), and
+//              wave 0 writes group_sizes / group_offsets / padded offsets;
+//   3. place:  each wave re-walks its range in order and writes pair p at
+//              hist[w][e] + rank, then advances the cursor;
+//   4. fill:   sentinel P in every padding row, block -> expert map.
 // ---------------------------------------------------------------------------
-constexpr int kAlignThreads = 1024;
-constexpr int kAlignWaves = kAlignThreads / 64;
+__device__ __forceinline__ uint64_t same_expert_mask(int e, bool ok, int nbits) {
+  uint64_t same = __ballot(ok);
+  for (int b = 0; b < nbits; ++b) {
+    const int bit = (e >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    same &= bit ? bal : ~bal;
+  }
+  return same;
+}
 
-__global__ __launch_bounds__(kAlignThreads) void align_kernel(
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void align_kernel(
     const int32_t* __restrict__ ids, int P, int E, int BM, int32_t* __restrict__ sorted_ids,
     int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
     int32_t* __restrict__ gpo) {
   extern __shared__ int sm[];
-  int* cnt = sm;                 // [E]
-  int* cur = sm + E;             // [E] next free row of each expert
-  int* pstart = sm + 2 * E;      // [E+1] padded offsets
-  // [kAlignWaves][E] per-wave counts of this chunk (<= 64, so one byte each)
-  unsigned char* wc = reinterpret_cast<unsigned char*>(sm + 3 * E + 1);
-  const int tid = threadIdx.x, l = lane_id(), wave = tid >> 6;
+  int* hist = sm;                 // [NW][E]
+  int* tot = sm + NW * E;         // [E]
+  int* pstart = tot + E;          // [E+1] padded offsets
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6;
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  const int R = ((P + NW - 1) / NW + 63) / 64 * 64;
+  const int p0 = w * R, p1 = min(P, p0 + R);
+  int* hw = hist + w * E;
 
-  for (int i = tid; i < E; i += kAlignThreads) cnt[i] = 0;
-  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wc[i] = 0;
-  __syncthreads();
-  for (int p = tid; p < P; p += kAlignThreads) {
-    const int e = ids[p];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[e], 1);  // out-of-range ids are dropped
+  for (int i = l; i < E; i += 64) hw[i] = 0;
+  // The walks load kU rounds of ids at once so one load latency is exposed per
+  // kU rounds, not per round.
+  constexpr int kU = 8;
+  // 1. count (the wave's own histogram row: no other wave touches it)
+  for (int base = p0; base < p1; base += 64 * kU) {
+    int ev[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int p = base + 64 * u + l;
+      ev[u] = p < p1 ? ids[p] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      int e = ev[u];
+      const bool ok = (unsigned)e < (unsigned)E;  // out-of-range ids are dropped
+      if (!ok) e = 0;
+      const uint64_t same = same_expert_mask(e, ok, nbits);
+      if (ok && __popcll(same & lt_mask) == 0) hw[e] += __popcll(same);
+    }
   }
   __syncthreads();
-
-  if (wave == 0) {
+  // 2. per-expert totals and per-wave exclusive prefix, then the expert scan
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = 0;
+    for (int v = 0; v < NW; ++v) {
+      const int c = hist[v * E + e];
+      hist[v * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (w == 0) {
     int carry = 0, carry_p = 0;
     for (int base = 0; base < E; base += 64) {
       const int e = base + l;
-      const int c = e < E ? cnt[e] : 0;
+      const int c = e < E ? tot[e] : 0;
       const int pc = (c + BM - 1) / BM * BM;
       int ic = c, ip = pc;  // inclusive scans
 #pragma unroll
@@ -162,7 +201,6 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(
         go[e] = carry + ic - c;
         gpo[e] = carry_p + ip - pc;
         pstart[e] = carry_p + ip - pc;
-        cur[e] = carry_p + ip - pc;
       }
       carry += __shfl(ic, 63);
       carry_p += __shfl(ip, 63);
@@ -174,43 +212,35 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(
     }
   }
   __syncthreads();
-
-  int nbits = 0;
-  while ((1 << nbits) < E) ++nbits;
-  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
-  for (int c0 = 0; c0 < P; c0 += kAlignThreads) {
-    const int p = c0 + tid;
-    int e = p < P ? ids[p] : -1;
-    const bool ok = (unsigned)e < (unsigned)E;
-    if (!ok) e = 0;
-    uint64_t same = __ballot(ok);
-    for (int b = 0; b < nbits; ++b) {
-      const int bit = (e >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      same &= bit ? bal : ~bal;
+  for (int e = tid; e < E; e += 64 * NW)
+    for (int v = 0; v < NW; ++v) hist[v * E + e] += pstart[e];
+  __syncthreads();
+  // 3. place, in pair order
+  for (int base = p0; base < p1; base += 64 * kU) {
+    int ev[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int p = base + 64 * u + l;
+      ev[u] = p < p1 ? ids[p] : -1;
     }
-    const int rank = __popcll(same & lt_mask);
-    const bool leader = ok && rank == 0;
-    const int n_same = __popcll(same);
-    if (leader) wc[wave * E + e] = (unsigned char)n_same;
-    __syncthreads();
-    if (ok) {
-      int prior = 0;
-      for (int w2 = 0; w2 < wave; ++w2) prior += (int)wc[w2 * E + e];
-      sorted_ids[cur[e] + prior + rank] = p;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int p = base + 64 * u + l;
+      int e = ev[u];
+      const bool ok = (unsigned)e < (unsigned)E;
+      if (!ok) e = 0;
+      const uint64_t same = same_expert_mask(e, ok, nbits);
+      const int rank = __popcll(same & lt_mask);
+      if (ok) {
+        const int dst = hw[e] + rank;
+        sorted_ids[dst] = p;
+        if (rank == 0) hw[e] = dst + __popcll(same);
+      }
     }
-    __syncthreads();
-    if (leader) {
-      atomicAdd(&cur[e], n_same);
-      wc[wave * E + e] = 0;
-    }
-    __syncthreads();
   }
-
-  // Padding rows -> sentinel P; blocks -> owning expert.
-  for (int e = wave; e < E; e += kAlignWaves) {
-    const int c = cnt[e];
-    const int lo = pstart[e] + c, hi = pstart[e + 1];
+  // 4. padding rows -> sentinel P; blocks -> owning expert (rows disjoint from 3)
+  for (int e = w; e < E; e += NW) {
+    const int lo = pstart[e] + tot[e], hi = pstart[e + 1];
     for (int r = lo + l; r < hi; r += 64) sorted_ids[r] = P;
     for (int b = pstart[e] / BM + l; b < hi / BM; b += 64) block_expert[b] = e;
   }
@@ -219,9 +249,16 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(
 hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
                         hipStream_t s) {
-  const size_t lds = sizeof(int) * (3 * (size_t)E + 1) + (size_t)kAlignWaves * E;
-  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), lds, s, ids, P, E, BM,
-                     sorted_ids, block_expert, gs, go, gpo);
+  // 16 waves while the histograms fit 48 KiB of LDS, else 8 (E <= 1024)
+  if (16 * E <= 12288) {
+    const size_t lds = sizeof(int) * (16 * (size_t)E + 2 * (size_t)E + 1);
+    hipLaunchKernelGGL(align_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, BM, sorted_ids,
+                       block_expert, gs, go, gpo);
+  } else {
+    const size_t lds = sizeof(int) * (8 * (size_t)E + 2 * (size_t)E + 1);
+    hipLaunchKernelGGL(align_kernel<8>, dim3(1), dim3(512), lds, s, ids, P, E, BM, sorted_ids,
+                       block_expert, gs, go, gpo);
+  }
   return hipGetLastError();
 }
 

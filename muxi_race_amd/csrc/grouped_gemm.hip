@@ -27,62 +27,96 @@ struct Layout {
   static_assert(NBM >= 1 && NBN >= 1, "wave tile must hold at least one 32x32 block");
 };
 
-template <int BM, int WAVES_M, int S, int NW, bool I8, bool GATHER>
+// Wave placement in a tile: the template layout for a BM-row item; a paired
+// item (2*BM rows, half the features) stacks twice the waves along M and half
+// along N, so every wave keeps the same WTM x WTN sub-tile.
+template <typename L>
+struct WavePos {
+  int wm, wn;
+  __device__ __forceinline__ WavePos(int wave, bool paired) {
+    const int wn_count = paired ? L::WAVES_N / 2 : L::WAVES_N;
+    wm = wave / wn_count;
+    wn = wave % wn_count;
+  }
+};
+
+// Runs f(std::integral_constant<int, NB>) with NB = min(live, MAX), live >= 0:
+// the K loops are instantiated per count of live 32-row token blocks.
+template <int MAX, typename F>
+__device__ __forceinline__ void with_live(int live, F&& f) {
+  if constexpr (MAX == 0) {
+    f(std::integral_constant<int, 0>{});
+  } else {
+    if (live >= MAX) f(std::integral_constant<int, MAX>{});
+    else with_live<MAX - 1>(live, f);
+  }
+}
+
+// One ring stage holds the tile's token rows, then its weight rows (Stage 1:
+// gate rows, then up rows), ROWS x 128 bytes in all, filled by one DmaTile;
+// fragment reads address it by stage row.
+template <int BM, int WAVES_M, int S, int NW, bool I8, bool GATHER, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using L = Layout<BM, WAVES_M, kBN, NW>;
   using Acc = typename std::conditional<I8, i32x16, f32x16>::type;
-  constexpr int XB = BM * kRowBytes;
-  constexpr int WB = kBN * kRowBytes;
-  constexpr int STAGE = XB + 2 * WB;
+  constexpr int ROWS = BM + 2 * kBN;
+  using LD = DmaTile<ROWS, NW>;
+  constexpr int STAGE = ROWS * kRowBytes;
+  static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
+  static_assert(!(PAIR && I8), "int8 quantises h per 128-column tile: items must span 128 columns");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
-  const int ntiles = (int)(p.I / kBN);
+  const int nt = (int)(p.I / kBN);
   Work w;
-  if (!schedule(blockIdx.x, p.gpo, p.E, BM, ntiles, p.host_blocks, false, w)) return;
+  if (!schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w)) return;
   const int e = w.e;
   const int gpo_e = p.gpo[e];
-  const int row0 = w.m_block * BM;
-  const int n0 = w.n_tile * kBN;
+  const int row0 = w.row0;
+  const int n0 = w.n0;
+  const int rx = PAIR ? w.rows : BM;   // token rows of the tile (stage rows [0, rx))
+  const int rw = PAIR ? w.bn : kBN;    // gate rows [rx, rx+rw), up rows [rx+rw, rx+2rw)
   int actual = p.gs[e] - (row0 - gpo_e);
-  actual = actual < 0 ? 0 : (actual > BM ? BM : actual);
+  actual = actual < 0 ? 0 : (actual > rx ? rx : actual);
   if (actual == 0) return;  // empty block: intermediate rows left untouched
 
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
 
-  DmaTile<BM, NW> xl;
-  DmaTile<kBN, NW> gl, ul;
+  LD ld;
 #pragma unroll
-  for (int i = 0; i < DmaTile<BM, NW>::NI; ++i) {
-    const int r = DmaTile<BM, NW>::row_of(i);
-    int64_t src_row;
-    if (GATHER) {
-      const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
-      src_row = pid / p.topk;
+  for (int i = 0; i < LD::NI; ++i) {
+    const int r = LD::row_of(i);
+    const char* src;
+    if (r < rx) {
+      int64_t src_row;
+      if (GATHER) {
+        const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
+        src_row = pid / p.topk;
+      } else {
+        src_row = row0 + r;
+      }
+      src = p.x + src_row * kbytes;
+    } else if (r < rx + rw) {
+      src = p.wg + ((int64_t)e * p.I + n0 + (r - rx)) * kbytes;
     } else {
-      src_row = row0 + r;
+      src = p.wu + ((int64_t)e * p.I + n0 + (r - rx - rw)) * kbytes;
     }
-    xl.set(i, p.x + src_row * kbytes);
-  }
-  const char* gbase = p.wg + ((int64_t)e * p.I + n0) * kbytes;
-  const char* ubase = p.wu + ((int64_t)e * p.I + n0) * kbytes;
-#pragma unroll
-  for (int i = 0; i < DmaTile<kBN, NW>::NI; ++i) {
-    const int r = DmaTile<kBN, NW>::row_of(i);
-    gl.set(i, gbase + r * kbytes);
-    ul.set(i, ubase + r * kbytes);
+    ld.set(i, src);
   }
 
   const int wave = threadIdx.x >> 6;
-  const int wm = wave / L::WAVES_N;
-  const int wn = wave % L::WAVES_N;
+  const WavePos<L> wp(wave, rx != BM);
+  const int wm = wp.wm, wn = wp.wn;
   // 32-row token blocks of this wave that hold at least one routed row
   // (wave-uniform); padding-only blocks skip their LDS reads and MFMAs.
   // (Skipping costs L2 sharing between the M blocks of one expert -- a block
   // with less MFMA work runs ahead of its siblings -- but measured faster
   // overall than keeping siblings in step.)
   const int live = (actual - wm * L::WTM + 31) / 32;
+  const int xr0 = wm * L::WTM;           // stage row of this wave's first token row
+  const int gr0 = rx + wn * L::WTN;      // ... of its first gate row
+  const int ur0 = rx + rw + wn * L::WTN; // ... of its first up row
   Acc ag[L::NBN][L::NBM], au[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -93,13 +127,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     }
 
   // S-stage ring: stages ks+1 .. ks+S-2 stay in flight while stage ks is used.
-  constexpr int Q = DmaTile<BM, NW>::NI + 2 * DmaTile<kBN, NW>::NI;  // loads per wave per stage
-  auto issue = [&](int buf, int k) {
-    char* st = smem + buf * STAGE;
-    xl.issue(st, k);
-    gl.issue(st + XB, k);
-    ul.issue(st + XB + WB, k);
-  };
+  constexpr int Q = LD::NI;  // loads per wave per stage
   // The K loop is instantiated per count NB of this wave's token blocks that
   // hold routed rows (chosen once, outside the loop: a branch inside it would
   // move the accumulators out of AGPRs every step); padding-only blocks get no
@@ -108,15 +136,13 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     constexpr int NB = decltype(nb_c)::value;
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
-      if (s < nk) issue(s, s);
+      if (s < nk) ld.issue(smem + s * STAGE, s);
     int cur = 0;
     for (int ks = 0; ks < nk; ++ks) {
       wait_stages<Q, S - 2>(nk - 1 - ks);
       barrier_no_fence();
-      if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
-      const char* cx = smem + cur * STAGE;
-      const char* cg = cx + XB;
-      const char* cu = cg + WB;
+      if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
+      const char* st = smem + cur * STAGE;
       cur = cur + 1 == S ? 0 : cur + 1;
       if constexpr (NB > 0) {
         // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
@@ -124,11 +150,11 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
         u32x4 xf[2][NB], gf[2][L::NBN], uf[2][L::NBN];
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) xf[buf][b] = frag(cx, wm * L::WTM + 32 * b, s);
+          for (int b = 0; b < NB; ++b) xf[buf][b] = frag(st, xr0 + 32 * b, s);
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a) {
-            gf[buf][a] = frag(cg, wn * L::WTN + 32 * a, s);
-            uf[buf][a] = frag(cu, wn * L::WTN + 32 * a, s);
+            gf[buf][a] = frag(st, gr0 + 32 * a, s);
+            uf[buf][a] = frag(st, ur0 + 32 * a, s);
           }
         };
         load_frags(0, 0);
@@ -148,9 +174,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       }
     }
   };
-  if (live >= L::NBM) main_loop(std::integral_constant<int, L::NBM>{});
-  else if (L::NBM > 1 && live >= 1) main_loop(std::integral_constant<int, 1>{});
-  else main_loop(std::integral_constant<int, 0>{});
+  with_live<L::NBM>(live < 0 ? 0 : live, main_loop);
   __syncthreads();  // every wave is done with the ring before LDS is reused
 
   const int l = lane_id();
@@ -158,7 +182,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     // h = silu(g) * u -> fp16, valid rows only (submission.py:1532-1542).
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
-      const int m = wm * L::WTM + 32 * b + (l & 31);
+      const int m = xr0 + 32 * b + (l & 31);
       if (m < actual) {
         _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.I;
 #pragma unroll
@@ -184,7 +208,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     const float* surow = p.su + (int64_t)e * p.I;
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
-      const int m = wm * L::WTM + 32 * b + (l & 31);
+      const int m = xr0 + 32 * b + (l & 31);
       float sx = 0.0f;
       if (m < actual) sx = p.x_scale[p.sorted_ids[row0 + m] / p.topk];
       float amax = 0.0f;
@@ -205,12 +229,12 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           }
         }
       amax = fmaxf(amax, __shfl_xor(amax, 32));
-      if (l < 32) red[wn * BM + wm * L::WTM + 32 * b + l] = amax;
+      if (l < 32) red[wn * BM + xr0 + 32 * b + l] = amax;
     }
     __syncthreads();
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
-      const int mrow = wm * L::WTM + 32 * b + (l & 31);
+      const int mrow = xr0 + 32 * b + (l & 31);
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < L::WAVES_N; ++j) amax = fmaxf(amax, red[j * BM + mrow]);
@@ -232,40 +256,145 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
             *reinterpret_cast<uint32_t*>(hrow + n) = packed;
           }
         // scales are stored block-major: [I/128][hs_stride]
-        if (wn == 0 && l < 32) p.h_scale[(int64_t)w.n_tile * p.hs_stride + grow] = amax / 127.0f;
+        if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = amax / 127.0f;
       }
     }
   }
 }
 
-template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED>
+// Stage 1 (fp16) for 32-row tiles with 64-wide gate / up tiles: twice the
+// items of the 128-wide tiles, for shapes with few items per CU (decode),
+// where the last round of workgroups would otherwise stream on a fraction of
+// the CUs.  Wave w computes one 32 x 32 block: gate (w < 2) or up (w >= 2),
+// features 32 * (w & 1) of the tile; the up waves hand their block to the
+// gate waves through LDS for the SiLU epilogue.
+template <int S>
+__global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
+  constexpr int BM = 32, BN = 64, NW = 4;
+  constexpr int ROWS = BM + 2 * BN;  // stage rows: tokens, gate rows, up rows
+  using LD = DmaTile<ROWS, NW>;
+  constexpr int STAGE = ROWS * kRowBytes;
+  static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
+  static_assert(S * STAGE >= 2 * 16 * 64 * 4, "the epilogue exchange reuses the ring");
+  __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
+
+  const int nt = (int)(p.I / BN);
+  Work w;
+  if (!schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, false, false, w)) return;
+  const int e = w.e;
+  const int row0 = w.row0;
+  const int n0 = w.n0;
+  int actual = p.gs[e] - (row0 - p.gpo[e]);
+  actual = actual < 0 ? 0 : (actual > BM ? BM : actual);
+  if (actual == 0) return;
+
+  const int64_t kbytes = p.H * 2;
+  const int nk = (int)(kbytes / kRowBytes);
+  LD ld;
+#pragma unroll
+  for (int i = 0; i < LD::NI; ++i) {
+    const int r = LD::row_of(i);
+    const char* src;
+    if (r < BM) {
+      const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
+      src = p.x + (int64_t)(pid / p.topk) * kbytes;
+    } else if (r < BM + BN) {
+      src = p.wg + ((int64_t)e * p.I + n0 + (r - BM)) * kbytes;
+    } else {
+      src = p.wu + ((int64_t)e * p.I + n0 + (r - BM - BN)) * kbytes;
+    }
+    ld.set(i, src);
+  }
+
+  const int wave = threadIdx.x >> 6;
+  const int mat = wave >> 1;  // 0: gate, 1: up
+  const int fb = wave & 1;    // 32-feature half of the tile
+  const int wr0 = BM + mat * BN + 32 * fb;
+  f32x16 acc = f32x16{};
+  constexpr int Q = LD::NI;
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) ld.issue(smem + s * STAGE, s);
+  int cur = 0;
+  for (int ks = 0; ks < nk; ++ks) {
+    wait_stages<Q, S - 2>(nk - 1 - ks);
+    barrier_no_fence();
+    if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
+    const char* st = smem + cur * STAGE;
+    cur = cur + 1 == S ? 0 : cur + 1;
+    u32x4 xf[2], wf[2];
+    xf[0] = frag(st, 0, 0);
+    wf[0] = frag(st, wr0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int b = s & 1;
+      if (s < 3) {
+        xf[b ^ 1] = frag(st, 0, s + 1);
+        wf[b ^ 1] = frag(st, wr0, s + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      acc = mma(wf[b], xf[b], acc);
+    }
+  }
+  __syncthreads();  // every wave is done with the ring before LDS is reused
+
+  // Accumulator register r of lane l holds the same (token, feature) in the
+  // gate and the up wave of one feature half, so the hand-over is by (r, l).
+  float* xu = reinterpret_cast<float*>(smem);  // [2 halves][16 regs][64 lanes]
+  const int l = lane_id();
+  if (mat == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) xu[(fb * 16 + r) * 64 + l] = acc[r];
+  }
+  __syncthreads();
+  if (mat == 0) {
+    const int m = l & 31;
+    if (m < actual) {
+      _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.I;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int n = n0 + 32 * fb + 8 * rg + 4 * (l >> 5);
+        f16x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (_Float16)silu_mul(acc[4 * rg + q], xu[(fb * 16 + 4 * rg + q) * 64 + l]);
+        *reinterpret_cast<f16x4*>(hrow + n) = v;
+      }
+    }
+  }
+}
+
+template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   using L = Layout<BM, WAVES_M, BN, NW>;
-  constexpr int XB = BM * kRowBytes;
-  constexpr int WB = BN * kRowBytes;
-  constexpr int STAGE = XB + WB + (I8 ? 256 * NW : 0);  // int8: + row scales of the step
+  constexpr int ROWS = BM + BN;
+  using LD = DmaTile<ROWS, NW>;
+  constexpr int SCALES = ROWS * kRowBytes;                // int8: row scales of the step
+  constexpr int STAGE = SCALES + (I8 ? 256 * NW : 0);
+  static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
-  const int ntiles = (int)(p.H / BN);
+  const int nt = (int)(p.H / BN);
   Work w;
-  if (!schedule(blockIdx.x, p.gpo, p.E, BM, ntiles, p.host_blocks, !FUSED, w)) return;
-  const int row0 = w.m_block * BM;
-  const int n0 = w.n_tile * BN;
+  if (!schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, !FUSED, PAIR, w)) return;
+  const int row0 = w.row0;
+  const int n0 = w.n0;
+  const int rx = PAIR ? w.rows : BM;  // token rows of the tile (stage rows [0, rx))
+  const int rw = PAIR ? w.bn : BN;    // weight rows [rx, rx+rw)
   int actual = 0, gpo_e = 0, go_e = 0;
   const int e = w.e;
   if (e >= 0) {
     gpo_e = p.gpo[e];
     go_e = FUSED ? 0 : p.go[e];
     actual = p.gs[e] - (row0 - gpo_e);
-    actual = actual < 0 ? 0 : (actual > BM ? BM : actual);
+    actual = actual < 0 ? 0 : (actual > rx ? rx : actual);
   }
   if (actual == 0) {
     if (!FUSED) {
       // Rows owned by no valid token are written as 0 (problem_detail.json:50 note 4).
       _Float16* o = reinterpret_cast<_Float16*>(p.out);
-      for (int idx = threadIdx.x; idx < BM * (BN / 8); idx += 64 * NW) {
-        const int r = idx / (BN / 8), c = idx % (BN / 8);
+      for (int idx = threadIdx.x; idx < rx * (rw / 8); idx += 64 * NW) {
+        const int r = idx / (rw / 8), c = idx % (rw / 8);
         *reinterpret_cast<u32x4*>(o + (int64_t)(row0 + r) * p.H + n0 + 8 * c) = u32x4{0, 0, 0, 0};
       }
     }
@@ -274,20 +403,21 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
-  DmaTile<BM, NW> al;
-  DmaTile<BN, NW> wl;
+  LD ld;
 #pragma unroll
-  for (int i = 0; i < DmaTile<BM, NW>::NI; ++i)
-    al.set(i, p.a + (int64_t)(row0 + DmaTile<BM, NW>::row_of(i)) * kbytes);
-  const char* wbase = p.wd + ((int64_t)e * p.H + n0) * kbytes;
-#pragma unroll
-  for (int i = 0; i < DmaTile<BN, NW>::NI; ++i) wl.set(i, wbase + DmaTile<BN, NW>::row_of(i) * kbytes);
+  for (int i = 0; i < LD::NI; ++i) {
+    const int r = LD::row_of(i);
+    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * kbytes
+                     : p.wd + ((int64_t)e * p.H + n0 + (r - rx)) * kbytes);
+  }
 
   const int wave = threadIdx.x >> 6;
-  const int wm = wave / L::WAVES_N;
-  const int wn = wave % L::WAVES_N;
+  const WavePos<L> wp(wave, rx != BM);
+  const int wm = wp.wm, wn = wp.wn;
   const int l = lane_id();
   const int live = (actual - wm * L::WTM + 31) / 32;  // see Stage 1
+  const int xr0 = wm * L::WTM;       // stage row of this wave's first token row
+  const int wr0 = rx + wn * L::WTN;  // ... of its first weight row
   f32x16 acc[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -300,15 +430,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   const float* scale_src = nullptr;
   if constexpr (I8) {
     const int r = 64 * wave_id() + l;
-    scale_src = p.a_scale + row0 + (r < BM ? r : 0);
+    scale_src = p.a_scale + row0 + (r < rx ? r : 0);
   }
-  constexpr int Q = DmaTile<BM, NW>::NI + DmaTile<BN, NW>::NI + (I8 ? 1 : 0);
+  constexpr int Q = LD::NI + (I8 ? 1 : 0);
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
-    al.issue(st, k);
-    wl.issue(st + XB, k);
-    if constexpr (I8)
-      dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + XB + WB + 256 * wave_id());
+    ld.issue(st, k);
+    if constexpr (I8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
   // K loop instantiated per count of live token blocks (see Stage 1).
   auto main_loop = [&](auto nb_c) {
@@ -321,16 +449,15 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       wait_stages<Q, S - 2>(nk - 1 - ks);
       barrier_no_fence();
       if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
-      const char* ca = smem + cur * STAGE;
-      const char* cw = ca + XB;
+      const char* st = smem + cur * STAGE;
       cur = cur + 1 == S ? 0 : cur + 1;
       if constexpr (NB > 0) {
         u32x4 af[2][NB], wf[2][L::NBN];
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) af[buf][b] = frag(ca, wm * L::WTM + 32 * b, s);
+          for (int b = 0; b < NB; ++b) af[buf][b] = frag(st, xr0 + 32 * b, s);
 #pragma unroll
-          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(cw, wn * L::WTN + 32 * a, s);
+          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(st, wr0 + 32 * a, s);
         };
         if constexpr (!I8) {
           load_frags(0, 0);
@@ -348,10 +475,10 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           // One K step of int8 is one 128-column scale block of the
           // intermediate: exact int32 partial product, then
           // acc += partial * s_h[row, block].
-          const float* scl = reinterpret_cast<const float*>(cw + WB);
+          const float* scl = reinterpret_cast<const float*>(st + SCALES);
           float sc[NB];
 #pragma unroll
-          for (int b = 0; b < NB; ++b) sc[b] = scl[wm * L::WTM + 32 * b + (l & 31)];
+          for (int b = 0; b < NB; ++b) sc[b] = scl[xr0 + 32 * b + (l & 31)];
           i32x16 ia[L::NBN][NB];
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a)
@@ -378,14 +505,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       }
     }
   };
-  if (live >= L::NBM) main_loop(std::integral_constant<int, L::NBM>{});
-  else if (L::NBM > 1 && live >= 1) main_loop(std::integral_constant<int, 1>{});
-  else main_loop(std::integral_constant<int, 0>{});
+  with_live<L::NBM>(live < 0 ? 0 : live, main_loop);
 
   _Float16* o = reinterpret_cast<_Float16*>(p.out);
 #pragma unroll
   for (int b = 0; b < L::NBM; ++b) {
-    const int m = wm * L::WTM + 32 * b + (l & 31);
+    const int m = xr0 + 32 * b + (l & 31);
     const bool valid = m < actual;
     float wr = 0.0f;
     int64_t orow = row0 + m;
@@ -467,10 +592,24 @@ constexpr int s2_stages(int bm) {
 #define MOE_S2_WAVES_128 8
 #endif
 
-template <int BM, int WM, int NW, bool I8, bool GATHER>
+// Pair the blocks of multi-block experts (one weight-tile read per two
+// blocks) in the 128-row instances; 0 turns pairing off.
+#ifndef MOE_PAIR
+#define MOE_PAIR 1
+#endif
+// fp16 Stage 1 of 32-row tiles: 64-wide gate / up tiles (1) or 128-wide (0),
+// and the ring depth of the narrow kernel (20 KiB stages).
+#ifndef MOE_S1_NARROW32
+#define MOE_S1_NARROW32 1
+#endif
+#ifndef MOE_S1N_STAGES
+#define MOE_S1N_STAGES 7
+#endif
+
+template <int BM, int WM, int NW, bool I8, bool GATHER, bool PAIR>
 static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
   constexpr int kS = s1_stages(BM);
-  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, NW, I8, GATHER>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, NW, I8, GATHER, PAIR>), dim3((unsigned)grid),
                      dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
@@ -478,21 +617,21 @@ static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
 // Stage 2's K loop is short (I / 64 steps), so its wide-M tiles take a
 // 256-wide N tile when H allows: half the workgroups, half the re-reads of the
 // intermediate, and twice the work behind each workgroup's pipeline fill and
-// epilogue.
-template <int BM, int WM, int BN, int NW, bool I8, bool FUSED>
+// epilogue.  Paired items are then 256 x 128.
+template <int BM, int WM, int BN, int NW, bool I8, bool FUSED, bool PAIR>
 static hipError_t go2(const Stage2Params& p, int64_t max_blocks, hipStream_t s) {
   constexpr int kS = s2_stages(BM);
   const int64_t grid = schedule_grid(max_blocks, p.H / BN);
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED, PAIR>), dim3((unsigned)grid),
                      dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
 template <bool I8, bool FUSED>
 static hipError_t go2_128(const Stage2Params& p, int64_t mb, hipStream_t s) {
   constexpr int NW = MOE_S2_WAVES_128;
-  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, NW, I8, FUSED>(p, mb, s);
-  return go2<128, 2, 128, NW, I8, FUSED>(p, mb, s);
+  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, NW, I8, FUSED, MOE_PAIR != 0>(p, mb, s);
+  return go2<128, 2, 128, NW, I8, FUSED, false>(p, mb, s);
 }
 
 hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, bool gather,
@@ -502,14 +641,24 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, boo
   const int64_t grid = schedule_grid(max_blocks, p.I / kBN);
   if (grid <= 0) return hipSuccess;
   constexpr int NW = MOE_S1_WAVES_128;
+  constexpr bool kPair = MOE_PAIR != 0;
   if (!gather) {
-    if (block_m == 128 && !int8) return go1<128, 2, NW, false, false>(p, grid, s);
+    if (block_m == 128 && !int8) return go1<128, 2, NW, false, false, kPair>(p, grid, s);
     return hipErrorInvalidValue;
   }
   switch (block_m) {
-    case 32: return int8 ? go1<32, 1, 4, true, true>(p, grid, s) : go1<32, 1, 4, false, true>(p, grid, s);
-    case 64: return int8 ? go1<64, 1, 4, true, true>(p, grid, s) : go1<64, 1, 4, false, true>(p, grid, s);
-    case 128: return int8 ? go1<128, 2, NW, true, true>(p, grid, s) : go1<128, 2, NW, false, true>(p, grid, s);
+    case 32:
+      if (int8) return go1<32, 1, 4, true, true, false>(p, grid, s);
+      if (MOE_S1_NARROW32) {
+        const int64_t g64 = schedule_grid(max_blocks, p.I / 64);
+        hipLaunchKernelGGL((stage1_narrow_kernel<MOE_S1N_STAGES>), dim3((unsigned)g64), dim3(256), 0, s, p);
+        return hipGetLastError();
+      }
+      return go1<32, 1, 4, false, true, false>(p, grid, s);
+    case 64:
+      return int8 ? go1<64, 1, 4, true, true, false>(p, grid, s) : go1<64, 1, 4, false, true, false>(p, grid, s);
+    case 128:
+      return int8 ? go1<128, 2, NW, true, true, false>(p, grid, s) : go1<128, 2, NW, false, true, kPair>(p, grid, s);
   }
   return hipErrorInvalidValue;
 }
@@ -524,8 +673,10 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, bool int8, boo
     return hipErrorInvalidValue;
   }
   switch (block_m) {
-    case 32: return int8 ? go2<32, 1, kBN, 4, true, true>(p, mb, s) : go2<32, 1, kBN, 4, false, true>(p, mb, s);
-    case 64: return int8 ? go2<64, 1, kBN, 4, true, true>(p, mb, s) : go2<64, 1, kBN, 4, false, true>(p, mb, s);
+    case 32:
+      return int8 ? go2<32, 1, kBN, 4, true, true, false>(p, mb, s) : go2<32, 1, kBN, 4, false, true, false>(p, mb, s);
+    case 64:
+      return int8 ? go2<64, 1, kBN, 4, true, true, false>(p, mb, s) : go2<64, 1, kBN, 4, false, true, false>(p, mb, s);
     case 128: return int8 ? go2_128<true, true>(p, mb, s) : go2_128<false, true>(p, mb, s);
   }
   return hipErrorInvalidValue;

@@ -168,43 +168,55 @@ __device__ __forceinline__ int quant_i8(float x, float inv) {
 }
 
 // ---------------------------------------------------------------------------
-// Work schedule.  A launch covers items (expert e, N tile n, M block m) of all
-// experts.  Items are numbered expert-major, then N tile, then M block, so the
-// M blocks of one expert that share a weight tile are adjacent; the item range
-// is cut into 8 contiguous chunks, one per XCD (workgroup g runs on XCD g % 8
-// and is that XCD's (g / 8)-th workgroup), so an expert's weight tiles and
-// token tiles are re-read from that XCD's L2 rather than from HBM.
-// M blocks of expert e are [gpo[e]/BM, gpo[e+1]/BM).  `host_blocks` is the
-// number of BM-row blocks the caller's buffers hold: expert blocks beyond it
-// are never scheduled (so inconsistent metadata cannot move an access out of
-// the buffers), and with `tail` set, blocks between the experts' last block
-// and host_blocks are scheduled as tail items (e = -1) covering padded rows
-// that no expert owns.
+// Work schedule.  A launch covers the BM-row blocks of all experts times the
+// nt output-feature tiles of width BN.  M blocks of expert e are
+// [gpo[e]/BM, gpo[e+1]/BM); `host_blocks` is the number of BM-row blocks the
+// caller's buffers hold: expert blocks beyond it are never scheduled (so
+// inconsistent metadata cannot move an access out of the buffers), and with
+// `tail` set, blocks between the experts' last block and host_blocks are
+// scheduled as tail items (e = -1) covering padded rows that no expert owns.
+//
+// Pairing.  With `pair` set, two consecutive blocks of one expert form one
+// item of 2*BM rows x BN/2 features instead of two items of BM x BN: the same
+// LDS stage (2*BM + 2*(BN/2) = BM + 2*BN rows when BN = BM) and the same MFMA
+// work, but the expert's weight tile is streamed once for both blocks instead
+// of once per block.  An expert of nb blocks then has P = nb/2 paired blocks
+// and nb%2 single blocks; either way it yields nb * nt items.  Its items are
+// ordered by N tile t: the 2P paired items of the two half tiles of t, then
+// the single block's item of t, so all items reading one weight tile are
+// adjacent.
+//
+// Items are numbered expert-major and the item range is cut into 8
+// contiguous chunks, one per XCD (workgroup g runs on XCD g % 8 and is that
+// XCD's (g / 8)-th workgroup), so the items sharing a weight tile or a token
+// tile run close together on one XCD and re-read it from that XCD's L2.
 // ---------------------------------------------------------------------------
 struct Work {
   int e;        // expert, or -1 for a tail block owned by no expert
-  int n_tile;
-  int m_block;
-  int blocks;   // M blocks of expert e (workgroups sharing this weight tile)
+  int row0;     // first row of the tile (in the expert-sorted row space)
+  int rows;     // BM, or 2*BM for a paired item
+  int n0;       // first output feature of the tile
+  int bn;       // BN, or BN/2 for a paired item
 };
 
-__device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM,
-                                         int ntiles, int host_blocks, bool tail, Work& w) {
+__device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
+                                         int nt, int host_blocks, bool tail, bool pair, Work& w) {
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
   const int total_blocks = tail ? host_blocks : expert_blocks;
-  const int total = total_blocks * ntiles;
+  const int total = total_blocks * nt;
   const int per = (total + kNumXcd - 1) / kNumXcd;
   const int slot = g / kNumXcd;
   const int v = (g % kNumXcd) * per + slot;
   if (slot >= per || v >= total) return false;
-  const int expert_items = expert_blocks * ntiles;
+  const int expert_items = expert_blocks * nt;
   if (v >= expert_items) {
     const int t = v - expert_items;
     w.e = -1;
-    w.m_block = expert_blocks + t / ntiles;
-    w.n_tile = t % ntiles;
-    w.blocks = 1;
+    w.row0 = (expert_blocks + t / nt) * BM;
+    w.rows = BM;
+    w.n0 = (t % nt) * BN;
+    w.bn = BN;
     return true;
   }
   // e = (number of experts whose first item is <= v) - 1, found with ballots.
@@ -213,20 +225,31 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
   for (int base = 0; base < E; base += 64) {
     const int e = base + l;
     int le = 0;
-    if (e < E) le = (gpo[e] / BM) * ntiles <= v;
+    if (e < E) le = (gpo[e] / BM) * nt <= v;
     cnt += __popcll(__ballot(le));
   }
   const int e = cnt - 1;
   if (e < 0) return false;  // only with inconsistent metadata (gpo[0] > 0)
   const int b0 = gpo[e] / BM;
-  const int mb = gpo[e + 1] / BM - b0;
-  if (mb <= 0) return false;
-  const int local = v - b0 * ntiles;
+  const int nb = gpo[e + 1] / BM - b0;
+  if (nb <= 0) return false;
+  const int local = v - b0 * nt;
+  const int t = local / nb;  // N tile
+  const int r = local % nb;  // item within tile t
+  const int P = pair ? nb / 2 : 0;
   w.e = e;
-  w.n_tile = local / mb;
-  w.m_block = b0 + local % mb;
-  w.blocks = mb;
-  return w.m_block >= 0 && w.m_block < host_blocks && w.n_tile < ntiles;
+  if (r < 2 * P) {
+    w.rows = 2 * BM;
+    w.row0 = (b0 + 2 * (r % P)) * BM;
+    w.bn = BN / 2;
+    w.n0 = (2 * t + r / P) * (BN / 2);
+  } else {
+    w.rows = BM;
+    w.row0 = (b0 + r) * BM;
+    w.bn = BN;
+    w.n0 = t * BN;
+  }
+  return (w.row0 + w.rows) / BM <= host_blocks && t < nt;
 }
 
 // Upper bound on the workgroups `schedule` needs for `blocks` M blocks.

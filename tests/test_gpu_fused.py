@@ -64,7 +64,7 @@ def test_edge_single_token_and_single_expert():
     _check(inp, what="T=1")
     inp = moe_inputs("small", 7, T=300)
     inp["logits"][:, 3] += 100.0  # every token picks expert 3 first -> 3 blocks of one expert
-    _check(inp, what="one hot expert")
+    _check(inp, block_m=128, what="one hot expert")
 
 
 def test_repeat_is_bitwise_deterministic():

@@ -63,7 +63,7 @@ def _align_both(ids_np, E, bm):
 
 
 @pytest.mark.parametrize("name", list(CONFIGS))
-@pytest.mark.parametrize("bm", [32, 128])
+@pytest.mark.parametrize("bm", [32, 128, 256])
 def test_align_bit_exact(name, bm):
     logits, bias, k, E = _logits_for(name, 200)
     rid, _ = route_topk(logits.cpu().numpy(), k, None if bias is None else bias.cpu().numpy())

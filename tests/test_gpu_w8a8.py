@@ -28,10 +28,11 @@ def test_quantize_rows_bit_exact():
     np.testing.assert_array_equal(q[1, :4].cpu().numpy(), [127, 3, -3, 1])
 
 
-def _run(inp, sample=None):
+def _run(inp, sample=None, block_m=0):
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"])
-    out = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw)
+    out = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw,
+                    block_m=block_m)
     torch.cuda.synchronize()
     T = inp["T"]
     rows = torch.arange(T) if sample is None else torch.from_numpy(
@@ -50,8 +51,9 @@ def _run(inp, sample=None):
     return rel
 
 
-def test_w8a8_small():
-    _run(moe_inputs("small", 21))
+@pytest.mark.parametrize("bm", [0, 32, 128])
+def test_w8a8_small(bm):
+    _run(moe_inputs("small", 21), block_m=bm)
 
 
 def test_w8a8_config_sampled():

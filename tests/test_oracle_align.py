@@ -43,7 +43,7 @@ def test_align_known_answer():
     np.testing.assert_array_equal(al["group_padded_offsets"], [0, 4, 8, 12])
 
 
-@pytest.mark.parametrize("T,k,E,bm", [(1, 1, 1, 128), (50, 2, 8, 32), (300, 8, 64, 128), (7, 3, 300, 64)])
+@pytest.mark.parametrize("T,k,E,bm", [(1, 1, 1, 128), (50, 2, 8, 32), (300, 8, 64, 128), (7, 3, 300, 64), (700, 8, 16, 256)])
 def test_align_invariants(rng, T, k, E, bm):
     ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
     al = align(ids, E, bm)
@@ -71,7 +71,7 @@ def test_align_capacity_bound(rng):
         E = int(rng.integers(1, 64))
         k = int(rng.integers(1, min(E, 8) + 1))
         T = int(rng.integers(0, 200))
-        bm = int(rng.choice([32, 64, 128]))
+        bm = int(rng.choice([32, 64, 128, 256]))
         ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32) \
             if T else np.zeros((0, k), np.int32)
         al = align(ids, E, bm)

@@ -262,20 +262,25 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   }
 }
 
-// Stage 1 (fp16) for 32-row tiles with 64-wide gate / up tiles: twice the
-// items of the 128-wide tiles, for shapes with few items per CU (decode),
-// where the last round of workgroups would otherwise stream on a fraction of
-// the CUs.  Wave w computes one 32 x 32 block: gate (w < 2) or up (w >= 2),
-// features 32 * (w & 1) of the tile; the up waves hand their block to the
-// gate waves through LDS for the SiLU epilogue.
-template <int S>
+// Stage 1 (fp16) for 32-row tiles with narrow gate / up tiles (BN = 64 or
+// 32 features each): two or four times the items of the 128-wide tiles, for
+// shapes with few items per CU (decode), where the last round of workgroups
+// would otherwise stream on a fraction of the CUs.  Each of the 4 waves owns
+// one 32 x 32 accumulator: gate (waves 0, 1) or up (waves 2, 3), and
+//   BN = 64: features 32 * (w & 1) of the tile, all 4 K sub-steps of a step;
+//   BN = 32: all 32 features, K sub-steps 2 * (w & 1) and 2 * (w & 1) + 1,
+//            the two halves summed in the epilogue.
+// The other accumulators reach the wave writing h through LDS.
+template <int BN, int S>
 __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
-  constexpr int BM = 32, BN = 64, NW = 4;
+  constexpr int BM = 32, NW = 4;
+  static_assert(BN == 64 || BN == 32, "narrow tiles are 64 or 32 features wide");
+  constexpr bool KSPLIT = BN == 32;
   constexpr int ROWS = BM + 2 * BN;  // stage rows: tokens, gate rows, up rows
   using LD = DmaTile<ROWS, NW>;
   constexpr int STAGE = ROWS * kRowBytes;
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
-  static_assert(S * STAGE >= 2 * 16 * 64 * 4, "the epilogue exchange reuses the ring");
+  static_assert(S * STAGE >= 4 * 16 * 64 * 4, "the epilogue exchange reuses the ring");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
   const int nt = (int)(p.I / BN);
@@ -308,29 +313,32 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
 
   const int wave = threadIdx.x >> 6;
   const int mat = wave >> 1;  // 0: gate, 1: up
-  const int fb = wave & 1;    // 32-feature half of the tile
-  const int wr0 = BM + mat * BN + 32 * fb;
+  const int half = wave & 1;  // feature half (BN = 64) or K half (BN = 32)
+  const int wr0 = BM + mat * BN + (KSPLIT ? 0 : 32 * half);
+  constexpr int SUB = KSPLIT ? 2 : 4;    // K sub-steps per wave per step
+  const int s0 = KSPLIT ? 2 * half : 0;  // first of them
   f32x16 acc = f32x16{};
+  const int stream_from = w.shared ? kNoStream : BM;  // weight rows no other item reads: streamed
   constexpr int Q = LD::NI;
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    if (s < nk) ld.issue(smem + s * STAGE, s);
+    if (s < nk) ld.issue(smem + s * STAGE, s, stream_from);
   int cur = 0;
   for (int ks = 0; ks < nk; ++ks) {
     wait_stages<Q, S - 2>(nk - 1 - ks);
     barrier_no_fence();
-    if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
+    if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1, stream_from);
     const char* st = smem + cur * STAGE;
     cur = cur + 1 == S ? 0 : cur + 1;
     u32x4 xf[2], wf[2];
-    xf[0] = frag(st, 0, 0);
-    wf[0] = frag(st, wr0, 0);
+    xf[0] = frag(st, 0, s0);
+    wf[0] = frag(st, wr0, s0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < SUB; ++s) {
       const int b = s & 1;
-      if (s < 3) {
-        xf[b ^ 1] = frag(st, 0, s + 1);
-        wf[b ^ 1] = frag(st, wr0, s + 1);
+      if (s + 1 < SUB) {
+        xf[b ^ 1] = frag(st, 0, s0 + s + 1);
+        wf[b ^ 1] = frag(st, wr0, s0 + s + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       acc = mma(wf[b], xf[b], acc);
@@ -338,32 +346,48 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
   }
   __syncthreads();  // every wave is done with the ring before LDS is reused
 
-  // Accumulator register r of lane l holds the same (token, feature) in the
-  // gate and the up wave of one feature half, so the hand-over is by (r, l).
-  float* xu = reinterpret_cast<float*>(smem);  // [2 halves][16 regs][64 lanes]
+  // Accumulator register r of lane l holds the same (token, feature) in every
+  // wave that covers the same features, so the hand-over is by (r, l):
+  // slot(w, r) for the waves other than the one writing h.
+  float* xs = reinterpret_cast<float*>(smem);
   const int l = lane_id();
-  if (mat == 1) {
+  auto slot = [&](int wv, int r) -> float& { return xs[(wv * 16 + r) * 64 + l]; };
+  const bool writer = KSPLIT ? wave == 0 : mat == 0;
+  if (!writer) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) xu[(fb * 16 + r) * 64 + l] = acc[r];
+    for (int r = 0; r < 16; ++r) slot(wave, r) = acc[r];
   }
   __syncthreads();
-  if (mat == 0) {
+  if (writer) {
     const int m = l & 31;
     if (m < actual) {
       _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.I;
+      const int fbase = KSPLIT ? 0 : 32 * half;
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
-        const int n = n0 + 32 * fb + 8 * rg + 4 * (l >> 5);
+        const int n = n0 + fbase + 8 * rg + 4 * (l >> 5);
         f16x4 v;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = (_Float16)silu_mul(acc[4 * rg + q], xu[(fb * 16 + 4 * rg + q) * 64 + l]);
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * rg + q;
+          float g, u;
+          if constexpr (KSPLIT) {  // waves: 0 gate k0, 1 gate k1, 2 up k0, 3 up k1
+            g = acc[r] + slot(1, r);
+            u = slot(2, r) + slot(3, r);
+          } else {                 // waves: 0/1 gate halves, 2/3 up halves
+            g = acc[r];
+            u = slot(2 + half, r);
+          }
+          v[q] = (_Float16)silu_mul(g, u);
+        }
         *reinterpret_cast<f16x4*>(hrow + n) = v;
       }
     }
   }
 }
 
-template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED, bool PAIR>
+// STREAM: weight tiles no other item reads are loaded non-temporal.
+template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED, bool PAIR, bool STREAM>
 __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   using L = Layout<BM, WAVES_M, BN, NW>;
   constexpr int ROWS = BM + BN;
@@ -435,7 +459,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   constexpr int Q = LD::NI + (I8 ? 1 : 0);
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
-    ld.issue(st, k);
+    if constexpr (STREAM) ld.issue(st, k, w.shared ? kNoStream : rx);
+    else ld.issue(st, k);
     if constexpr (I8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
   // K loop instantiated per count of live token blocks (see Stage 1).
@@ -597,13 +622,13 @@ constexpr int s2_stages(int bm) {
 #ifndef MOE_PAIR
 #define MOE_PAIR 1
 #endif
-// fp16 Stage 1 of 32-row tiles: 64-wide gate / up tiles (1) or 128-wide (0),
-// and the ring depth of the narrow kernel (20 KiB stages).
+// fp16 Stage 1 of 32-row tiles: gate / up tile width of the narrow kernel
+// (64 or 32; 0 = the 128-wide tiles) and its ring depth.
 #ifndef MOE_S1_NARROW32
-#define MOE_S1_NARROW32 1
+#define MOE_S1_NARROW32 32
 #endif
 #ifndef MOE_S1N_STAGES
-#define MOE_S1N_STAGES 7
+#define MOE_S1N_STAGES 6
 #endif
 
 template <int BM, int WM, int NW, bool I8, bool GATHER, bool PAIR>
@@ -623,7 +648,7 @@ static hipError_t go2(const Stage2Params& p, int64_t max_blocks, hipStream_t s) 
   constexpr int kS = s2_stages(BM);
   const int64_t grid = schedule_grid(max_blocks, p.H / BN);
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED, PAIR>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED, PAIR, BM == 32>), dim3((unsigned)grid),
                      dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
@@ -649,9 +674,10 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, boo
   switch (block_m) {
     case 32:
       if (int8) return go1<32, 1, 4, true, true, false>(p, grid, s);
-      if (MOE_S1_NARROW32) {
-        const int64_t g64 = schedule_grid(max_blocks, p.I / 64);
-        hipLaunchKernelGGL((stage1_narrow_kernel<MOE_S1N_STAGES>), dim3((unsigned)g64), dim3(256), 0, s, p);
+      if constexpr (MOE_S1_NARROW32 != 0) {
+        constexpr int kW = MOE_S1_NARROW32;
+        const int64_t gn = schedule_grid(max_blocks, p.I / kW);
+        hipLaunchKernelGGL((stage1_narrow_kernel<kW, MOE_S1N_STAGES>), dim3((unsigned)gn), dim3(256), 0, s, p);
         return hipGetLastError();
       }
       return go1<32, 1, 4, false, true, false>(p, grid, s);

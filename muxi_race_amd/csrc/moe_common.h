@@ -87,19 +87,36 @@ __device__ __forceinline__ void barrier_no_fence() {
 
 #define MOE_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-// global_load_lds_dword[x4]: per-lane global address -> LDS at m0 + 4|16 * lane.
-// The host compilation pass only needs kernel signatures (for the launch
-// stubs); the builtin is kept out of that pass, where clang's deferred
-// diagnostic for it otherwise stops the remaining kernel stubs from being
-// emitted.
-template <int BYTES>
+// Cache policy of weight loads that no other tile repeats, used by the
+// decode-sized (32-row) kernels.  A weight tile read by exactly one item is
+// loaded non-temporal (the gfx950 `nt` bit, cache-policy immediate 2):
+// measured on a load-ring probe, streaming reads rise from 6.06 to 6.84 TB/s
+// (rows 14 KiB apart) and from 5.71 to 6.35 TB/s (4 KiB apart), and decode
+// from 0.575 to 0.533 ms.  Weight tiles that sibling items of a multi-block
+// expert re-read from L2, and token / intermediate rows, keep the default
+// policy (non-temporal there measured slower: fewer L2 hits); the wide-tile
+// kernels load everything with the default policy (no gain measured there,
+// and the per-instruction choice cost 2-5%).  0 turns streaming off.
+#ifndef MOE_W_POLICY
+#define MOE_W_POLICY 2
+#endif
+constexpr int kPolicyDefault = 0;
+constexpr int kPolicyWeights = MOE_W_POLICY;
+constexpr int kNoStream = 1 << 30;  // `weights_from` that streams no row
+
+// global_load_lds_dword[x4]: per-lane global address -> LDS at m0 + 4|16 * lane,
+// cache policy POLICY.  The host compilation pass only needs kernel
+// signatures (for the launch stubs); the builtin is kept out of that pass,
+// where clang's deferred diagnostic for it otherwise stops the remaining
+// kernel stubs from being emitted.
+template <int BYTES, int POLICY = kPolicyDefault>
 __device__ __forceinline__ void dma_to_lds(const void* g, void* lds) {
   static_assert(BYTES == 4 || BYTES == 16, "dword or dwordx4");
 #if defined(__HIP_DEVICE_COMPILE__)
   if constexpr (BYTES == 16)
-    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 16, 0, POLICY);
   else
-    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, MOE_LDS_PTR(lds), 4, 0, POLICY);
 #else
   (void)g;
   (void)lds;
@@ -128,8 +145,21 @@ struct DmaTile {
   __device__ __forceinline__ void issue(char* lds, int ks) const {
     const int w = wave_id();
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-      dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+    for (int i = 0; i < NI; ++i) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+  }
+  // As issue(), with tile rows from `weights_from` on loaded under the
+  // streaming weight policy (kNoStream: none); an instruction's 8 rows never
+  // straddle that boundary when it is a multiple of 8, so the choice is
+  // wave-uniform.
+  __device__ __forceinline__ void issue(char* lds, int ks, int weights_from) const {
+    const int w = wave_id();
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const char* g = src[i] + (size_t)ks * kRowBytes;
+      char* d = lds + 1024 * (NW * i + w);
+      if (8 * (NW * i + w) >= weights_from) dma_to_lds<16, kPolicyWeights>(g, d);
+      else dma_to_lds<16>(g, d);
+    }
   }
 };
 
@@ -197,6 +227,7 @@ struct Work {
   int rows;     // BM, or 2*BM for a paired item
   int n0;       // first output feature of the tile
   int bn;       // BN, or BN/2 for a paired item
+  bool shared;  // other items of this launch read the same weight rows
 };
 
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
@@ -217,6 +248,7 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
     w.rows = BM;
     w.n0 = (t % nt) * BN;
     w.bn = BN;
+    w.shared = false;
     return true;
   }
   // e = (number of experts whose first item is <= v) - 1, found with ballots.
@@ -238,6 +270,7 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
   const int r = local % nb;  // item within tile t
   const int P = pair ? nb / 2 : 0;
   w.e = e;
+  w.shared = pair ? nb > 2 : nb > 1;
   if (r < 2 * P) {
     w.rows = 2 * BM;
     w.row0 = (b0 + 2 * (r % P)) * BM;

@@ -253,7 +253,7 @@ def main():
     ideal_ms = max(flops / (peak_c * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
     s1_hbm_bound = s1_bytes / (PEAK_HBM_GBS * 1e9) >= s1_flops / (peak_c * 1e12)
     s1_traffic = recorded_traffic(args.config + ("_w8a8" if w8 and args.config != "w8a8" else ""),
-                                  "moe::stage1_kernel")
+                                  "moe::stage1")  # stage1_kernel / stage1_narrow_kernel
 
     check_res = None
     if not args.no_check:

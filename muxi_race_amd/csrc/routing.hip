@@ -264,7 +264,9 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
 
 // ---------------------------------------------------------------------------
 // Combine: out[t, :] = sum_j y_pair[t*k + j, :], fp32 in choice order -> fp16.
-// One thread per 8 output columns.
+// One thread per 8 output columns.  The k rows are loaded in batches of 8
+// before they are summed (in choice order), so each thread keeps several loads
+// in flight; y_pair is read once, so the loads are non-temporal.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y, int64_t T,
                                                       int64_t H, int k, _Float16* __restrict__ out) {
@@ -274,10 +276,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   const int64_t t = idx / cpr, c = idx % cpr;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const _Float16* src = y + (t * k) * H + 8 * c;
-  for (int j = 0; j < k; ++j) {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(src + (int64_t)j * H);
+  constexpr int kBatch = 8;
+  for (int j0 = 0; j0 < k; j0 += kBatch) {
+    f16x8 v[kBatch];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] += (float)v[q];
+    for (int u = 0; u < kBatch; ++u)
+      if (j0 + u < k) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)(j0 + u) * H));
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (j0 + u < k) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += (float)v[u][q];
+      }
   }
   f16x8 r;
 #pragma unroll

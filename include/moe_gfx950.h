@@ -86,11 +86,16 @@ int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E,
  * metadata in the reference's layout (remote_bench.py:82-101).  The number
  * of padded rows produced is group_padded_offsets[E].
  * capacity = moe_align_capacity_rows(T, k, E, block_m).  E <= 1024.
+ * scratch (device, moe_align_scratch_bytes(T, k, E) bytes, 16-byte aligned)
+ * lets large batches be aligned by many workgroups; NULL (or 0 bytes) runs
+ * one workgroup.  The result is identical either way.
  * ---------------------------------------------------------------------- */
 int64_t moe_align_capacity_rows(int64_t T, int64_t k, int64_t E, int64_t block_m);
+int64_t moe_align_scratch_bytes(int64_t T, int64_t k, int64_t E);
 int moe_align(const int32_t* topk_ids, int64_t T, int64_t k, int64_t E, int64_t block_m,
               int32_t* sorted_pair_ids, int32_t* block_expert, int32_t* group_sizes,
-              int32_t* group_offsets, int32_t* group_padded_offsets, void* stream);
+              int32_t* group_offsets, int32_t* group_padded_offsets, void* scratch,
+              int64_t scratch_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Full fused MoE (fp16): route -> align -> Stage1 (gathered gate/up GEMM +

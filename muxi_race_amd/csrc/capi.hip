@@ -35,7 +35,7 @@ int64_t cap_rows(int64_t T, int64_t k, int64_t E, int64_t bm) {
 }
 
 struct FusedLayout {
-  int64_t ids, w, sorted, bexp, gs, go, gpo, h, hs, xq, sx, ypair, total;
+  int64_t ids, w, sorted, bexp, gs, go, gpo, whist, h, hs, xq, sx, ypair, total;
 };
 
 FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm,
@@ -50,6 +50,7 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, 
   L.gs = o; o += up(E * 4);
   L.go = o; o += up((E + 1) * 4);
   L.gpo = o; o += up((E + 1) * 4);
+  L.whist = o; o += up((int64_t)moe::align_groups((int)P) * E * 4);  // align workgroup histograms
   L.h = o; o += up(rows * I * (w8 ? 1 : 2));
   L.hs = o; o += w8 ? up(rows * (I / moe::kBN) * 4) : 0;  // [I/128][rows], block-major
   L.xq = o; o += w8 ? up(T * H) : 0;
@@ -157,15 +158,27 @@ int64_t moe_align_capacity_rows(int64_t T, int64_t k, int64_t E, int64_t block_m
   return cap_rows(T, k, E, block_m);
 }
 
+int64_t moe_align_scratch_bytes(int64_t T, int64_t k, int64_t E) {
+  if (T < 0 || k <= 0 || E <= 0 || T * k >= ((int64_t)1 << 30)) return 0;
+  return (int64_t)moe::align_groups((int)(T * k)) * E * 4;
+}
+
 int moe_align(const int32_t* topk_ids, int64_t T, int64_t k, int64_t E, int64_t block_m,
               int32_t* sorted_pair_ids, int32_t* block_expert, int32_t* group_sizes,
-              int32_t* group_offsets, int32_t* group_padded_offsets, void* stream) {
+              int32_t* group_offsets, int32_t* group_padded_offsets, void* scratch,
+              int64_t scratch_bytes, void* stream) {
   if (T < 0 || k <= 0 || E <= 0 || block_m <= 0) return fail(MOE_ERR_INVALID_ARG, "bad sizes");
   if (E > 1024) return fail(MOE_ERR_UNSUPPORTED, "E=%lld > 1024", (long long)E);
   if (T * k >= ((int64_t)1 << 30)) return fail(MOE_ERR_UNSUPPORTED, "too many pairs");
   if ((T > 0 && (!topk_ids || !sorted_pair_ids || !block_expert)) || !group_sizes || !group_offsets || !group_padded_offsets)
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return check_launch(moe::launch_align(topk_ids, (int)(T * k), (int)E, (int)block_m, sorted_pair_ids, block_expert, group_sizes, group_offsets, group_padded_offsets, (hipStream_t)stream), "align");
+  int32_t* whist = nullptr;
+  if (scratch && scratch_bytes > 0) {
+    if (scratch_bytes < moe_align_scratch_bytes(T, k, E)) return fail(MOE_ERR_WORKSPACE, "align scratch %lld < %lld bytes", (long long)scratch_bytes, (long long)moe_align_scratch_bytes(T, k, E));
+    if (!aligned16(scratch)) return fail(MOE_ERR_INVALID_ARG, "align scratch must be 16-byte aligned");
+    whist = (int32_t*)scratch;
+  }
+  return check_launch(moe::launch_align(topk_ids, (int)(T * k), (int)E, (int)block_m, sorted_pair_ids, block_expert, group_sizes, group_offsets, group_padded_offsets, whist, (hipStream_t)stream), "align");
 }
 
 int64_t moe_pick_block_m(int64_t T, int64_t E, int64_t k) { return pick_bm(T, E, k); }
@@ -209,7 +222,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const float
   mark(0);
   if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s), "route_topk"))) return rc;
   mark(1);
-  if ((rc = check_launch(moe::launch_align(ids, (int)(T * k), (int)E, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, s), "align"))) return rc;
+  if ((rc = check_launch(moe::launch_align(ids, (int)(T * k), (int)E, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
   mark(2);
   if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, (int8_t*)(ws + L.xq), (float*)(ws + L.sx), s), "quantize_x"))) return rc;
   mark(3);

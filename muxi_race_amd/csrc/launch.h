@@ -55,9 +55,23 @@ hipError_t launch_stage2(const Stage2Params& p, int block_m, bool int8, bool fus
 
 hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
                              int32_t* ids, float* w, hipStream_t stream);
+// `whist` (int32 [align_groups(P) * E], may be null) lets a large P be aligned
+// by align_groups(P) workgroups in two launches instead of one workgroup.
+constexpr int kAlignPairsPerGroup = 2048;
+constexpr int kAlignMaxGroups = 64;
+// (below 4 groups' worth of pairs the second launch costs more than it saves)
+inline int align_groups(int P) {
+  const int g = (P + kAlignPairsPerGroup - 1) / kAlignPairsPerGroup;
+  return g < 4 ? 1 : (g > kAlignMaxGroups ? kAlignMaxGroups : g);
+}
+// pairs per workgroup: a multiple of 64 * nw covering P in `groups` workgroups
+inline int align_pairs_per_group(int P, int groups, int nw) {
+  const int per = (P + groups - 1) / groups;
+  return (per + 64 * nw - 1) / (64 * nw) * (64 * nw);
+}
 hipError_t launch_align(const int32_t* ids, int P, int E, int block_m, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
-                        hipStream_t stream);
+                        int32_t* whist, hipStream_t stream);
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream);
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,

@@ -131,100 +131,49 @@ __device__ __forceinline__ uint64_t same_expert_mask(int e, bool ok, int nbits) 
   return same;
 }
 
-template <int NW>
-__global__ __launch_bounds__(64 * NW) void align_kernel(
-    const int32_t* __restrict__ ids, int P, int E, int BM, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
-    int32_t* __restrict__ gpo) {
-  extern __shared__ int sm[];
-  int* hist = sm;                 // [NW][E]
-  int* tot = sm + NW * E;         // [E]
-  int* pstart = tot + E;          // [E+1] padded offsets
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6;
-  int nbits = 0;
-  while ((1 << nbits) < E) ++nbits;
-  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
-  const int R = ((P + NW - 1) / NW + 63) / 64 * 64;
-  const int p0 = w * R, p1 = min(P, p0 + R);
-  int* hw = hist + w * E;
+// Walks of one wave over its contiguous pair range [p0, p1).  The walks load
+// kU rounds of ids at once so one load latency is exposed per kU rounds, not
+// per round.  Out-of-range ids are dropped.
+constexpr int kAlignUnroll = 8;
 
+// count: the wave's private histogram hw[E] (no other wave touches it)
+__device__ __forceinline__ void align_count_range(const int32_t* __restrict__ ids, int p0, int p1, int E,
+                                                  int nbits, int* hw) {
+  const int l = lane_id();
   for (int i = l; i < E; i += 64) hw[i] = 0;
-  // The walks load kU rounds of ids at once so one load latency is exposed per
-  // kU rounds, not per round.
-  constexpr int kU = 8;
-  // 1. count (the wave's own histogram row: no other wave touches it)
-  for (int base = p0; base < p1; base += 64 * kU) {
-    int ev[kU];
+  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  for (int base = p0; base < p1; base += 64 * kAlignUnroll) {
+    int ev[kAlignUnroll];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kAlignUnroll; ++u) {
       const int p = base + 64 * u + l;
       ev[u] = p < p1 ? ids[p] : -1;
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kAlignUnroll; ++u) {
       int e = ev[u];
-      const bool ok = (unsigned)e < (unsigned)E;  // out-of-range ids are dropped
+      const bool ok = (unsigned)e < (unsigned)E;
       if (!ok) e = 0;
       const uint64_t same = same_expert_mask(e, ok, nbits);
       if (ok && __popcll(same & lt_mask) == 0) hw[e] += __popcll(same);
     }
   }
-  __syncthreads();
-  // 2. per-expert totals and per-wave exclusive prefix, then the expert scan
-  for (int e = tid; e < E; e += 64 * NW) {
-    int run = 0;
-    for (int v = 0; v < NW; ++v) {
-      const int c = hist[v * E + e];
-      hist[v * E + e] = run;
-      run += c;
-    }
-    tot[e] = run;
-  }
-  __syncthreads();
-  if (w == 0) {
-    int carry = 0, carry_p = 0;
-    for (int base = 0; base < E; base += 64) {
-      const int e = base + l;
-      const int c = e < E ? tot[e] : 0;
-      const int pc = (c + BM - 1) / BM * BM;
-      int ic = c, ip = pc;  // inclusive scans
+}
+
+// place, in pair order: pair p goes to hw[e] + rank, then the cursor advances
+__device__ __forceinline__ void align_place_range(const int32_t* __restrict__ ids, int p0, int p1, int E,
+                                                  int nbits, int* hw, int32_t* __restrict__ sorted_ids) {
+  const int l = lane_id();
+  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  for (int base = p0; base < p1; base += 64 * kAlignUnroll) {
+    int ev[kAlignUnroll];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int a = __shfl_up(ic, o), b = __shfl_up(ip, o);
-        if (l >= o) {
-          ic += a;
-          ip += b;
-        }
-      }
-      if (e < E) {
-        gs[e] = c;
-        go[e] = carry + ic - c;
-        gpo[e] = carry_p + ip - pc;
-        pstart[e] = carry_p + ip - pc;
-      }
-      carry += __shfl(ic, 63);
-      carry_p += __shfl(ip, 63);
-    }
-    if (l == 0) {
-      go[E] = carry;
-      gpo[E] = carry_p;
-      pstart[E] = carry_p;
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += 64 * NW)
-    for (int v = 0; v < NW; ++v) hist[v * E + e] += pstart[e];
-  __syncthreads();
-  // 3. place, in pair order
-  for (int base = p0; base < p1; base += 64 * kU) {
-    int ev[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kAlignUnroll; ++u) {
       const int p = base + 64 * u + l;
       ev[u] = p < p1 ? ids[p] : -1;
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kAlignUnroll; ++u) {
       const int p = base + 64 * u + l;
       int e = ev[u];
       const bool ok = (unsigned)e < (unsigned)E;
@@ -238,19 +187,195 @@ __global__ __launch_bounds__(64 * NW) void align_kernel(
       }
     }
   }
-  // 4. padding rows -> sentinel P; blocks -> owning expert (rows disjoint from 3)
-  for (int e = w; e < E; e += NW) {
+}
+
+// Expert scan by one wave: tot[E] -> padded offsets pstart[E+1] in LDS, and
+// (when `out`) group sizes / offsets / padded offsets in global memory.
+__device__ __forceinline__ void align_expert_scan(const int* tot, int E, int BM, int* pstart, bool out,
+                                                  int32_t* __restrict__ gs, int32_t* __restrict__ go,
+                                                  int32_t* __restrict__ gpo) {
+  const int l = lane_id();
+  int carry = 0, carry_p = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + l;
+    const int c = e < E ? tot[e] : 0;
+    const int pc = (c + BM - 1) / BM * BM;
+    int ic = c, ip = pc;  // inclusive scans
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(ic, o), b = __shfl_up(ip, o);
+      if (l >= o) {
+        ic += a;
+        ip += b;
+      }
+    }
+    if (e < E) {
+      pstart[e] = carry_p + ip - pc;
+      if (out) {
+        gs[e] = c;
+        go[e] = carry + ic - c;
+        gpo[e] = carry_p + ip - pc;
+      }
+    }
+    carry += __shfl(ic, 63);
+    carry_p += __shfl(ip, 63);
+  }
+  if (l == 0) {
+    pstart[E] = carry_p;
+    if (out) {
+      go[E] = carry;
+      gpo[E] = carry_p;
+    }
+  }
+}
+
+// padding rows of experts e0, e0 + step, ... -> sentinel P; their blocks ->
+// owning expert (rows disjoint from the placed ones); by one wave
+__device__ __forceinline__ void align_fill(const int* pstart, const int* tot, int E, int BM, int P, int e0,
+                                           int step, int32_t* __restrict__ sorted_ids,
+                                           int32_t* __restrict__ block_expert) {
+  const int l = lane_id();
+  for (int e = e0; e < E; e += step) {
     const int lo = pstart[e] + tot[e], hi = pstart[e + 1];
     for (int r = lo + l; r < hi; r += 64) sorted_ids[r] = P;
     for (int b = pstart[e] / BM + l; b < hi / BM; b += 64) block_expert[b] = e;
   }
 }
 
+__device__ __forceinline__ int bits_for(int E) {
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  return nbits;
+}
+
+// One workgroup of NW waves; wave w owns the contiguous pair range
+// [w*R, (w+1)*R).  1. count into per-wave histograms; 2. per-wave exclusive
+// prefix per expert and the expert scan; 3. place; 4. fill.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void align_kernel(
+    const int32_t* __restrict__ ids, int P, int E, int BM, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
+    int32_t* __restrict__ gpo) {
+  extern __shared__ int sm[];
+  int* hist = sm;                 // [NW][E]
+  int* tot = sm + NW * E;         // [E]
+  int* pstart = tot + E;          // [E+1] padded offsets
+  const int tid = threadIdx.x, w = tid >> 6;
+  const int nbits = bits_for(E);
+  const int R = ((P + NW - 1) / NW + 63) / 64 * 64;
+  const int p0 = w * R, p1 = min(P, p0 + R);
+  int* hw = hist + w * E;
+  align_count_range(ids, p0, p1, E, nbits, hw);
+  __syncthreads();
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = 0;
+    for (int v = 0; v < NW; ++v) {
+      const int c = hist[v * E + e];
+      hist[v * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (w == 0) align_expert_scan(tot, E, BM, pstart, true, gs, go, gpo);
+  __syncthreads();
+  for (int e = tid; e < E; e += 64 * NW)
+    for (int v = 0; v < NW; ++v) hist[v * E + e] += pstart[e];
+  __syncthreads();
+  align_place_range(ids, p0, p1, E, nbits, hw, sorted_ids);
+  align_fill(pstart, tot, E, BM, P, w, NW, sorted_ids, block_expert);
+}
+
+// Large P: G workgroups, workgroup g owning pairs [g*RW, (g+1)*RW) (wave w of
+// it the sub-range [w*R, (w+1)*R)).  Kernel 1 writes each workgroup's expert
+// histogram to whist[g][E]; kernel 2 derives from all of them the expert scan
+// and the workgroup's first row per expert, recounts per wave, and places.
+// Pair order within an expert, hence the output, is the one-workgroup kernel's.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void align_count_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                              int RW, int32_t* __restrict__ whist) {
+  extern __shared__ int sm[];
+  int* hist = sm;  // [NW][E]
+  const int tid = threadIdx.x, w = tid >> 6;
+  const int g0 = blockIdx.x * RW, g1 = min(P, g0 + RW);
+  const int R = RW / NW;
+  const int p0 = min(g1, g0 + w * R), p1 = min(g1, p0 + R);
+  align_count_range(ids, p0, p1, E, bits_for(E), hist + w * E);
+  __syncthreads();
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = 0;
+    for (int v = 0; v < NW; ++v) run += hist[v * E + e];
+    whist[(int64_t)blockIdx.x * E + e] = run;
+  }
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void align_place_kernel(
+    const int32_t* __restrict__ ids, int P, int E, int BM, int RW, const int32_t* __restrict__ whist,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ block_expert, int32_t* __restrict__ gs,
+    int32_t* __restrict__ go, int32_t* __restrict__ gpo) {
+  extern __shared__ int sm[];
+  int* hist = sm;                 // [NW][E]
+  int* tot = sm + NW * E;         // [E]
+  int* pstart = tot + E;          // [E+1]
+  int* before = pstart + E + 1;   // [E] pairs of expert e in the workgroups before this one
+  const int tid = threadIdx.x, w = tid >> 6;
+  const int G = gridDim.x, g = blockIdx.x;
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = 0, mine = 0;
+    for (int v = 0; v < G; ++v) {
+      const int c = whist[(int64_t)v * E + e];
+      if (v == g) mine = run;
+      run += c;
+    }
+    tot[e] = run;
+    before[e] = mine;
+  }
+  const int g0 = g * RW, g1 = min(P, g0 + RW);
+  const int R = RW / NW;
+  const int p0 = min(g1, g0 + w * R), p1 = min(g1, p0 + R);
+  const int nbits = bits_for(E);
+  int* hw = hist + w * E;
+  align_count_range(ids, p0, p1, E, nbits, hw);
+  __syncthreads();
+  if (w == 0) align_expert_scan(tot, E, BM, pstart, g == 0, gs, go, gpo);
+  __syncthreads();
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = pstart[e] + before[e];
+    for (int v = 0; v < NW; ++v) {
+      const int c = hist[v * E + e];
+      hist[v * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  align_place_range(ids, p0, p1, E, nbits, hw, sorted_ids);
+  align_fill(pstart, tot, E, BM, P, g * NW + w, G * NW, sorted_ids, block_expert);
+}
+
 hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
-                        hipStream_t s) {
+                        int32_t* whist, hipStream_t s) {
   // 16 waves while the histograms fit 48 KiB of LDS, else 8 (E <= 1024)
-  if (16 * E <= 12288) {
+  const bool w16 = 16 * E <= 12288;
+  const int G = align_groups(P);
+  if (whist && G > 1) {
+    const int NW = w16 ? 16 : 8;
+    const int RW = align_pairs_per_group(P, G, NW);
+    const size_t lds1 = sizeof(int) * ((size_t)NW * E);
+    const size_t lds2 = sizeof(int) * ((size_t)NW * E + 3 * (size_t)E + 1);
+    if (w16) {
+      hipLaunchKernelGGL(align_count_kernel<16>, dim3(G), dim3(1024), lds1, s, ids, P, E, RW, whist);
+      hipLaunchKernelGGL(align_place_kernel<16>, dim3(G), dim3(1024), lds2, s, ids, P, E, BM, RW, whist,
+                         sorted_ids, block_expert, gs, go, gpo);
+    } else {
+      hipLaunchKernelGGL(align_count_kernel<8>, dim3(G), dim3(512), lds1, s, ids, P, E, RW, whist);
+      hipLaunchKernelGGL(align_place_kernel<8>, dim3(G), dim3(512), lds2, s, ids, P, E, BM, RW, whist,
+                         sorted_ids, block_expert, gs, go, gpo);
+    }
+    return hipGetLastError();
+  }
+  if (w16) {
     const size_t lds = sizeof(int) * (16 * (size_t)E + 2 * (size_t)E + 1);
     hipLaunchKernelGGL(align_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, BM, sorted_ids,
                        block_expert, gs, go, gpo);
@@ -306,8 +431,21 @@ hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void*
 }
 
 // ---------------------------------------------------------------------------
-// Per-row symmetric int8: one wave per row, 8 fp16 per lane per step.
+// Per-row symmetric int8: one wave per row, 8 fp16 per lane per chunk.  Rows
+// of up to 64 * 8 * NCH elements are held in registers (all NCH chunk loads
+// in flight at once, one pass over memory); longer rows take two passes.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x2 quant_pack8(f16x8 v, float inv) {
+  u32x2 packed = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int qv = quant_i8((float)v[i], inv);
+    packed[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+  }
+  return packed;
+}
+
+template <int NCH>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ w, int64_t R,
                                                          int64_t K, int8_t* __restrict__ q,
                                                          float* __restrict__ scale) {
@@ -315,24 +453,36 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
   const int l = lane_id();
   if (r >= R) return;
   const _Float16* row = w + r * K;
-  float amax = 0.0f;
-  for (int64_t c = 8 * l; c < K; c += 512) {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
-  }
-  amax = wave_max(amax);
-  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
   int8_t* qrow = q + r * K;
-  for (int64_t c = 8 * l; c < K; c += 512) {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
-    u32x2 packed = {0u, 0u};
+  float amax = 0.0f;
+  if constexpr (NCH > 0) {
+    f16x8 v[NCH];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int qv = quant_i8((float)v[i], inv);
-      packed[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * l;
+      v[j] = c < K ? *reinterpret_cast<const f16x8*>(row + c) : f16x8{};
     }
-    *reinterpret_cast<u32x2*>(qrow + c) = packed;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[j][i]));
+    amax = wave_max(amax);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int64_t c = 512 * j + 8 * l;
+      if (c < K) *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8(v[j], inv);
+    }
+  } else {
+    for (int64_t c = 8 * l; c < K; c += 512) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
+    }
+    amax = wave_max(amax);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    for (int64_t c = 8 * l; c < K; c += 512)
+      *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8(*reinterpret_cast<const f16x8*>(row + c), inv);
   }
   if (l == 0) scale[r] = amax / 127.0f;
 }
@@ -340,8 +490,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
                              hipStream_t s) {
   if (R == 0) return hipSuccess;
-  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s,
-                     reinterpret_cast<const _Float16*>(w), R, K, q, scale);
+  const dim3 grid((unsigned)((R + 3) / 4)), block(256);
+  const _Float16* src = reinterpret_cast<const _Float16*>(w);
+  const int64_t nch = (K + 511) / 512;
+  if (nch <= 4) hipLaunchKernelGGL(quant_rows_kernel<4>, grid, block, 0, s, src, R, K, q, scale);
+  else if (nch <= 8) hipLaunchKernelGGL(quant_rows_kernel<8>, grid, block, 0, s, src, R, K, q, scale);
+  else if (nch <= 16) hipLaunchKernelGGL(quant_rows_kernel<16>, grid, block, 0, s, src, R, K, q, scale);
+  else hipLaunchKernelGGL(quant_rows_kernel<0>, grid, block, 0, s, src, R, K, q, scale);
   return hipGetLastError();
 }
 

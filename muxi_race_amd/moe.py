@@ -131,11 +131,13 @@ def route_topk(router_logits: torch.Tensor, top_k: int, expert_bias: torch.Tenso
     return ids, w
 
 
-def moe_align(topk_ids: torch.Tensor, num_experts: int, block_m: int):
+def moe_align(topk_ids: torch.Tensor, num_experts: int, block_m: int, many_workgroups: bool = True):
     """Expert-sorted, block-padded pair permutation (see include/moe_gfx950.h).
 
     Returns a dict of device int32 tensors sized to the capacity bound;
-    ``group_padded_offsets[E]`` is the number of rows actually used.
+    ``group_padded_offsets[E]`` is the number of rows actually used.  With
+    ``many_workgroups`` a large batch is aligned by several workgroups (a
+    scratch buffer is allocated for it); the result is identical either way.
     """
     _need(topk_ids, "topk_ids", (torch.int32,), 2)
     dev = topk_ids.device
@@ -147,9 +149,12 @@ def moe_align(topk_ids: torch.Tensor, num_experts: int, block_m: int):
     gs = torch.empty(num_experts, dtype=torch.int32, device=dev)
     go = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
     gpo = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    nscratch = int(L.moe_align_scratch_bytes(T, k, num_experts)) if many_workgroups else 0
+    scratch = torch.empty(max(nscratch, 16), dtype=torch.uint8, device=dev) if nscratch else None
     with torch.cuda.device(dev):
         rc = L.moe_align(_ptr(topk_ids), T, k, num_experts, block_m, _ptr(sorted_ids), _ptr(bexp),
-                         _ptr(gs), _ptr(go), _ptr(gpo), _stream(dev))
+                         _ptr(gs), _ptr(go), _ptr(gpo), _ptr(scratch) if nscratch else None, nscratch,
+                         _stream(dev))
     check(rc, "moe_align")
     return dict(sorted_pair_ids=sorted_ids, block_expert=bexp, group_sizes=gs, group_offsets=go,
                 group_padded_offsets=gpo)

@@ -49,9 +49,9 @@ def test_routing_ties(E, k):
     np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
 
 
-def _align_both(ids_np, E, bm):
+def _align_both(ids_np, E, bm, many_workgroups=True):
     from muxi_race_amd import moe_align
-    got = moe_align(torch.from_numpy(ids_np).cuda(), E, bm)
+    got = moe_align(torch.from_numpy(ids_np).cuda(), E, bm, many_workgroups=many_workgroups)
     torch.cuda.synchronize()
     ref = align(ids_np, E, bm)
     rows = int(ref["group_padded_offsets"][-1])
@@ -64,10 +64,11 @@ def _align_both(ids_np, E, bm):
 
 @pytest.mark.parametrize("name", list(CONFIGS))
 @pytest.mark.parametrize("bm", [32, 128, 256])
-def test_align_bit_exact(name, bm):
+@pytest.mark.parametrize("many", [True, False])  # several workgroups (large P) or one
+def test_align_bit_exact(name, bm, many):
     logits, bias, k, E = _logits_for(name, 200)
     rid, _ = route_topk(logits.cpu().numpy(), k, None if bias is None else bias.cpu().numpy())
-    _align_both(rid, E, bm)
+    _align_both(rid, E, bm, many)
 
 
 def test_align_edges():
@@ -76,4 +77,21 @@ def test_align_edges():
     _align_both(np.array([[5]], np.int32), 1024, 64)              # one pair, E = 1024
     _align_both(np.zeros((0, 2), np.int32), 8, 128)               # no tokens
     ids = np.stack([rng.choice(1024, 8, replace=False) for _ in range(5000)]).astype(np.int32)
-    _align_both(ids, 1024, 32)                                     # many chunks, wide E
+    _align_both(ids, 1024, 32)                                     # many chunks, wide E (8 waves)
+    _align_both(np.full((70000, 2), 7, np.int32), 16, 128)         # 64 workgroups, one hot expert
+
+
+def test_align_many_workgroups_matches_one_on_dropped_ids():
+    """Out-of-range ids are dropped (the oracle rejects them): both GPU paths
+    must still agree bit for bit on a ragged batch spread over 14 workgroups."""
+    from muxi_race_amd import moe_align
+    ids = torch.from_numpy(np.random.default_rng(1).integers(-3, 19, (9001, 3)).astype(np.int32)).cuda()
+    a = moe_align(ids, 16, 64, many_workgroups=True)
+    b = moe_align(ids, 16, 64, many_workgroups=False)
+    torch.cuda.synchronize()
+    rows = int(b["group_padded_offsets"][-1])
+    assert int(a["group_padded_offsets"][-1]) == rows
+    assert torch.equal(a["sorted_pair_ids"][:rows], b["sorted_pair_ids"][:rows])
+    assert torch.equal(a["block_expert"][:rows // 64], b["block_expert"][:rows // 64])
+    for key in ("group_sizes", "group_offsets", "group_padded_offsets"):
+        assert torch.equal(a[key], b[key])

@@ -13,10 +13,11 @@ pytestmark = pytest.mark.gpu
 W8A8_REL_L2 = 5e-2
 
 
-def test_quantize_rows_bit_exact():
+@pytest.mark.parametrize("K", [1024, 2048 + 8, 7168, 8200])  # register path (4, 8, 16 chunks) and two-pass
+def test_quantize_rows_bit_exact(K):
     from muxi_race_amd import quantize_rows_w8
-    g = torch.Generator().manual_seed(0)
-    w = (torch.randn(300, 1024, generator=g) * 0.02).half()
+    g = torch.Generator().manual_seed(K)
+    w = (torch.randn(300, K, generator=g) * 0.02).half()
     w[0] = 0.0
     w[1, :4] = torch.tensor([127.0, 2.5, -2.5, 0.5]).half()
     w[1, 4:] = 0.0

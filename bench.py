@@ -150,6 +150,9 @@ def main():
     ap.add_argument("--no-check", action="store_true", help="skip the sampled oracle check")
     ap.add_argument("--w8a8", action="store_true", help="run the int8 path (default for --config w8a8)")
     ap.add_argument("--fp16", action="store_true", help="run the fp16 path even for --config w8a8")
+    ap.add_argument("--router-gemm", action="store_true",
+                    help="also time the router GEMM + routing (x . w_router^T, seeded w_router) alone and "
+                         "the fused step started from hidden states (moe_fused_forward_hidden); fp16 only")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -281,6 +284,43 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
 
+    router = None
+    if args.router_gemm and not w8:
+        # router weight [E, H] ~ N(0, 1/H): logits ~ N(0, 1) like the configs' synthetic logits
+        gr = torch.Generator(device=dev).manual_seed(SEED + 2)
+        wr = (torch.randn((E, H), generator=gr, device=dev) / H ** 0.5).half()
+        rws = torch.empty(max(int(L.moe_router_workspace_bytes(T, H, E)), 256), dtype=torch.uint8, device=dev)
+        rargs = [P(inp["x"].data_ptr()), P(wr.data_ptr()), head[2], T, H, E, k, P(ids.data_ptr()),
+                 P(wts.data_ptr()), P(0), P(rws.data_ptr()), rws.numel(), stream]
+        hws = torch.empty(int(L.moe_fused_hidden_workspace_bytes(T, H, I, E, k, bm)), dtype=torch.uint8,
+                          device=dev)
+        hargs = [P(inp["x"].data_ptr()), P(wr.data_ptr()), head[2]] + \
+                [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + \
+                [P(out.data_ptr()), T, H, I, E, k, bm, P(hws.data_ptr()), hws.numel(), P(ids.data_ptr()),
+                 P(wts.data_ptr()), stream]
+
+        def timed(fn, fargs, label):
+            for _ in range(args.warmup):
+                check(fn(*fargs), label)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            for _ in range(args.steps):
+                check(fn(*fargs), label)
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / args.steps
+
+        r_ms = timed(L.moe_route_hidden, rargs, "moe_route_hidden")
+        h_ms = timed(L.moe_fused_forward_hidden, hargs, "moe_fused_forward_hidden")
+        r_flops = 2.0 * T * H * E
+        r_bytes = (T * H + E * H) * 2.0 + T * k * 8
+        router = {"router_ms": round(r_ms, 4), "router_tflops": round(r_flops / (r_ms * 1e-3) / 1e12, 2),
+                  "router_gb_per_s": round(r_bytes / (r_ms * 1e-3) / 1e9, 1),
+                  "router_roofline_frac": round(max(r_flops / (PEAK_F16_TFLOPS * 1e12),
+                                                    r_bytes / (PEAK_HBM_GBS * 1e9)) / (r_ms * 1e-3), 4),
+                  "fused_from_hidden_ms": round(h_ms, 4)}
+
     copy_gbs = None
     if args.calib_copy:
         n = 1 << 29  # 1 GiB of fp16 read + 1 GiB written per copy
@@ -346,6 +386,8 @@ def main():
         res["calib_copy_gb_per_s"] = copy_gbs
     if quant_ms is not None:
         res["weight_quantisation_ms_once"] = round(quant_ms, 3)
+    if router is not None:
+        res["router"] = router
     print(json.dumps(res), flush=True)
 
 

@@ -79,6 +79,21 @@ int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E,
                    int32_t* topk_ids, float* topk_weights, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Router GEMM upstream of the top-k (no reference counterpart: the
+ * reference's operator receives routed tokens, problem_detail.json:18/:30).
+ * moe_route_hidden: logits = x . w_router^T (x fp16 [T, H], w_router fp16
+ * [E, H], fp32 accumulation; H a multiple of 128, E <= 1024,
+ * k <= min(E, 32)), then exactly moe_route_topk's softmax / top-k /
+ * renormalisation of logits + bias.  logits_out (fp32 [T, E]) may be NULL.
+ * workspace: moe_router_workspace_bytes(T, H, E) bytes (K-split partial
+ * sums, summed in split order: the result is deterministic).
+ * ---------------------------------------------------------------------- */
+int64_t moe_router_workspace_bytes(int64_t T, int64_t H, int64_t E);
+int moe_route_hidden(const void* x, const void* w_router, const float* bias, int64_t T, int64_t H,
+                     int64_t E, int64_t k, int32_t* topk_ids, float* topk_weights, float* logits_out,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * moe_align: counting sort of the P = T*k routed pairs (p = t*k + j) by
  * expert, ascending pair order inside an expert, each expert padded to a
  * multiple of block_m rows with the sentinel P.  Writes sorted_pair_ids
@@ -125,6 +140,17 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events);
+
+/* moe_fused_forward_hidden: moe_fused_forward with the router GEMM
+ * (moe_route_hidden) in place of precomputed logits: x fp16 [T, H],
+ * w_router fp16 [E, H]; workspace moe_fused_hidden_workspace_bytes bytes. */
+int64_t moe_fused_hidden_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                         int64_t block_m);
+int moe_fused_forward_hidden(const void* x, const void* w_router, const float* bias, const void* w_gate,
+                             const void* w_up, const void* w_down, void* out, int64_t T, int64_t H,
+                             int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
+                             int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
+                             void* stream);
 
 /* ------------------------------------------------------------------------
  * W8A8.  moe_quantize_rows_w8: per-row symmetric int8 of an fp16 [R, K]

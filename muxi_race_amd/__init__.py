@@ -15,6 +15,7 @@ from .moe import (  # noqa: F401
     pick_block_m,
     quantize_rows_w8,
     quantize_w8a8_weights,
+    route_hidden,
     route_topk,
     run_kernel,
 )

@@ -29,6 +29,11 @@ SIGNATURES = {
     "moe_route_topk": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "moe_align_capacity_rows": (_i64, [_i64, _i64, _i64, _i64]),
     "moe_align_scratch_bytes": (_i64, [_i64, _i64, _i64]),
+    "moe_router_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "moe_route_hidden": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p]),
+    "moe_fused_hidden_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "moe_fused_forward_hidden": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _p, _i64, _p, _p, _p]),
     "moe_align": (_int, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "moe_fused_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _int]),
     "moe_pick_block_m": (_i64, [_i64, _i64, _i64]),

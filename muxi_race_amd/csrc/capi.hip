@@ -153,6 +153,32 @@ int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E,
   return check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, topk_ids, topk_weights, (hipStream_t)stream), "route_topk");
 }
 
+int64_t moe_router_workspace_bytes(int64_t T, int64_t H, int64_t E) {
+  if (T < 0 || H <= 0 || E <= 0 || H % 128) return 0;
+  return up(moe::router_partial_floats(T, H, E) * 4);
+}
+
+static int check_router(const void* x, const void* w_router, int64_t T, int64_t H, int64_t E, int64_t k) {
+  if (T < 0 || H <= 0 || E <= 0 || k <= 0) return fail(MOE_ERR_INVALID_ARG, "bad sizes T=%lld H=%lld E=%lld k=%lld", (long long)T, (long long)H, (long long)E, (long long)k);
+  if (H % 128) return fail(MOE_ERR_UNSUPPORTED, "H=%lld must be a multiple of 128", (long long)H);
+  if (E > 1024 || k > 32 || k > E) return fail(MOE_ERR_UNSUPPORTED, "need E <= 1024 and k <= min(E, 32)");
+  if (T * E >= ((int64_t)1 << 31)) return fail(MOE_ERR_UNSUPPORTED, "T*E too large");
+  if (T > 0 && (!x || !w_router)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (T > 0 && (!aligned16(x) || !aligned16(w_router))) return fail(MOE_ERR_INVALID_ARG, "x and w_router must be 16-byte aligned");
+  return MOE_OK;
+}
+
+int moe_route_hidden(const void* x, const void* w_router, const float* bias, int64_t T, int64_t H, int64_t E,
+                     int64_t k, int32_t* topk_ids, float* topk_weights, float* logits_out, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
+  int rc = check_router(x, w_router, T, H, E, k);
+  if (rc) return rc;
+  if (T == 0) return MOE_OK;
+  if (!topk_ids || !topk_weights || !workspace) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (workspace_bytes < moe_router_workspace_bytes(T, H, E)) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)moe_router_workspace_bytes(T, H, E));
+  return check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, topk_ids, topk_weights, logits_out, (float*)workspace, (hipStream_t)stream), "router");
+}
+
 int64_t moe_align_capacity_rows(int64_t T, int64_t k, int64_t E, int64_t block_m) {
   if (T < 0 || k <= 0 || E <= 0 || block_m <= 0) return 0;
   return cap_rows(T, k, E, block_m);
@@ -190,7 +216,7 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
   return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
 }
 
-static int fused_common(bool w8, const void* x, const float* logits, const float* bias,
+static int fused_common(bool w8, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
                         const void* wd, const float* sd, void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
@@ -200,12 +226,14 @@ static int fused_common(bool w8, const void* x, const float* logits, const float
   int rc = check_dims(T, H, I, E, k, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
-  if (!x || !logits || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
+  if (!x || (!logits && !w_router) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  if (w_router && (rc = check_router(x, w_router, T, H, E, k))) return rc;
   if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
   const FusedLayout L = fused_layout(T, H, I, E, k, block_m, w8);
-  if (workspace_bytes < L.total) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)L.total);
+  const int64_t need = L.total + (w_router ? moe_router_workspace_bytes(T, H, E) : 0);
+  if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);
@@ -220,7 +248,11 @@ static int fused_common(bool w8, const void* x, const float* logits, const float
   // [4] stage 1, [5] stage 2, [6] combined
   auto mark = [&](int i) { if (ev && ev[i]) (void)hipEventRecord((hipEvent_t)ev[i], s); };
   mark(0);
-  if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s), "route_topk"))) return rc;
+  if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
+    if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s), "router"))) return rc;
+  } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s), "route_topk"))) {
+    return rc;
+  }
   mark(1);
   if ((rc = check_launch(moe::launch_align(ids, (int)(T * k), (int)E, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
   mark(2);
@@ -275,7 +307,24 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias, con
                       int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                       int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                       void* stream) {
-  return fused_common(false, x, logits, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+                      T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
+                      topk_weights_out, stream, nullptr);
+}
+
+int64_t moe_fused_hidden_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                         int64_t block_m) {
+  const int64_t f = moe_fused_workspace_bytes(T, H, I, E, k, block_m, 0);
+  return f ? f + moe_router_workspace_bytes(T, H, E) : 0;
+}
+
+int moe_fused_forward_hidden(const void* x, const void* w_router, const float* bias, const void* w_gate,
+                             const void* w_up, const void* w_down, void* out, int64_t T, int64_t H,
+                             int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
+                             int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
+                             void* stream) {
+  if (!w_router && T > 0) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -286,7 +335,7 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events) {
-  return fused_common(false, x, logits, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }
@@ -306,7 +355,7 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                            void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                            int64_t block_m, void* workspace, int64_t workspace_bytes,
                            int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
-  return fused_common(true, x, logits, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -318,7 +367,7 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int64_t block_m, void* workspace, int64_t workspace_bytes,
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events) {
-  return fused_common(true, x, logits, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }

@@ -72,6 +72,13 @@ inline int align_pairs_per_group(int P, int groups, int nw) {
 hipError_t launch_align(const int32_t* ids, int P, int E, int block_m, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
                         int32_t* whist, hipStream_t stream);
+// Router GEMM (x . w_router^T, K split in router_splits parts) + routing of
+// the summed partials; `part` holds router_partial_floats fp32, `logits`
+// (fp32 [T, E]) may be null.
+int router_splits(int64_t T, int64_t H, int64_t E);
+int64_t router_partial_floats(int64_t T, int64_t H, int64_t E);
+hipError_t launch_router(const void* x, const void* w_router, const float* bias, int T, int64_t H, int E,
+                         int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t stream);
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream);
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,

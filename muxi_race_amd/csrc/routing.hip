@@ -4,21 +4,9 @@
 // on the order in which atomics land.
 #include "launch.h"
 #include "moe_common.h"
-
-#include <math.h>
+#include "route_token.h"
 
 namespace moe {
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
 
 // ---------------------------------------------------------------------------
 // Router: one wave per token, VPL = ceil(E/64) logits per lane.
@@ -29,69 +17,9 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          int E, int k, int32_t* __restrict__ ids,
                                                          float* __restrict__ wout) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int l = lane_id();
   if (t >= T) return;  // uniform per wave
   const float* row = logits + (int64_t)t * E;
-  float v[VPL];
-  uint32_t valid = 0;
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int e = l + 64 * j;
-    v[j] = -INFINITY;
-    if (e < E) {
-      float x = row[e];
-      if (bias) x = x + bias[e];
-      v[j] = x;
-      valid |= 1u << j;
-      m = fmaxf(m, x);
-    }
-  }
-  m = wave_max(m);
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (valid & (1u << j)) s += expf(v[j] - m);
-  s = wave_sum(s);
-
-  uint32_t taken = 0;
-  float my_p = 0.0f;
-  int my_id = 0;
-  float denom = 0.0f;
-  constexpr int kNone = 0x7fffffff;
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int be = kNone;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const uint32_t bit = 1u << j;
-      if ((valid & bit) && !(taken & bit) && (be == kNone || v[j] > bv)) {
-        bv = v[j];
-        be = l + 64 * j;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oe = __shfl_xor(be, o);
-      const bool take = oe != kNone && (be == kNone || ov > bv || (ov == bv && oe < be));
-      if (take) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    if ((be & 63) == l) taken |= 1u << (be >> 6);
-    const float pr = expf(bv - m) / s;
-    denom = denom + pr;  // selection order, identical in every lane
-    if (l == r) {
-      my_p = pr;
-      my_id = be;
-    }
-  }
-  if (l < k) {
-    ids[(int64_t)t * k + l] = my_id;
-    wout[(int64_t)t * k + l] = my_p / denom;
-  }
+  route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout);
 }
 
 hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,

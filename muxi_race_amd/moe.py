@@ -21,7 +21,7 @@ import torch
 from ._lib import MoeError, check, lib
 
 __all__ = [
-    "run_kernel", "fused_moe", "route_topk", "moe_align", "quantize_rows_w8",
+    "run_kernel", "fused_moe", "route_topk", "route_hidden", "moe_align", "quantize_rows_w8",
     "W8A8Weights", "quantize_w8a8_weights", "fused_workspace_bytes", "pick_block_m", "MoeError",
 ]
 
@@ -131,6 +131,36 @@ def route_topk(router_logits: torch.Tensor, top_k: int, expert_bias: torch.Tenso
     return ids, w
 
 
+def route_hidden(hidden_states: torch.Tensor, router_weight: torch.Tensor, top_k: int,
+                 expert_bias: torch.Tensor | None = None, return_logits: bool = False):
+    """Router GEMM + routing: logits = hidden_states . router_weight^T (fp16
+    inputs, fp32 accumulation), then route_topk's softmax / top-k /
+    renormalisation.  Returns (ids, weights) or (ids, weights, logits)."""
+    x, wr = hidden_states, router_weight
+    _need(x, "hidden_states", (torch.float16,), 2)
+    dev = x.device
+    _need(wr, "router_weight", (torch.float16,), 2, dev)
+    T, H = x.shape
+    E = wr.shape[0]
+    if wr.shape[1] != H:
+        raise ValueError("router_weight must be [E, H]")
+    if expert_bias is not None:
+        _need(expert_bias, "expert_bias", (torch.float32,), 1, dev)
+        if expert_bias.numel() != E:
+            raise ValueError("expert_bias must have E entries")
+    L = lib()
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev) if return_logits else None
+    nbytes = int(L.moe_router_workspace_bytes(T, H, E))
+    ws = _workspace(dev, ("router",), nbytes) if nbytes else None
+    with torch.cuda.device(dev):
+        rc = L.moe_route_hidden(_ptr(x), _ptr(wr), _ptr(expert_bias), T, H, E, top_k, _ptr(ids), _ptr(w),
+                                _ptr(logits), _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
+    check(rc, "route_hidden")
+    return (ids, w, logits) if return_logits else (ids, w)
+
+
 def moe_align(topk_ids: torch.Tensor, num_experts: int, block_m: int, many_workgroups: bool = True):
     """Expert-sorted, block-padded pair permutation (see include/moe_gfx950.h).
 
@@ -208,20 +238,32 @@ def quantize_w8a8_weights(w_gate, w_up, w_down) -> W8A8Weights:
 # ---------------------------------------------------------------------------
 def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
               expert_bias=None, w8a8: W8A8Weights | None = None, block_m: int = 0, out=None,
-              return_routing: bool = False):
+              return_routing: bool = False, router_weight=None):
     """Full MoE FFN: softmax/top-k/renormalise routing, expert SwiGLU MLPs,
     routing-weighted combine.  hidden_states fp16 [T, H], router_logits fp32
     [T, E], w_gate/w_up fp16 [E, I, H], w_down fp16 [E, H, I] (or ``w8a8``
     quantised weights, in which case w_gate/w_up/w_down may be None).
+    With ``router_weight`` (fp16 [E, H]) and router_logits None (fp16 path
+    only), the logits are computed in the same call by the router GEMM.
     Returns fp16 [T, H] (and (ids, weights) when ``return_routing``)."""
     x = hidden_states
     _need(x, "hidden_states", (torch.float16,), 2)
     dev = x.device
     T, H = x.shape
-    _need(router_logits, "router_logits", (torch.float32,), 2, dev)
-    E = router_logits.shape[1]
-    if router_logits.shape[0] != T:
-        raise ValueError("router_logits rows != tokens")
+    if router_weight is not None:
+        if router_logits is not None:
+            raise ValueError("give router_logits or router_weight, not both")
+        if w8a8 is not None:
+            raise ValueError("router_weight is supported on the fp16 path")
+        _need(router_weight, "router_weight", (torch.float16,), 2, dev)
+        E = router_weight.shape[0]
+        if router_weight.shape[1] != H:
+            raise ValueError("router_weight must be [E, H]")
+    else:
+        _need(router_logits, "router_logits", (torch.float32,), 2, dev)
+        E = router_logits.shape[1]
+        if router_logits.shape[0] != T:
+            raise ValueError("router_logits rows != tokens")
     if w8a8 is None:
         for name, t in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down)):
             _need(t, name, (torch.float16,), 3, dev)
@@ -253,12 +295,19 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
             raise ValueError("out shape mismatch")
     L = lib()
     bm = block_m or int(L.moe_pick_block_m(T, E, top_k))
-    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, top_k, bm, int(w8a8 is not None))
+    if router_weight is not None:
+        nbytes = L.moe_fused_hidden_workspace_bytes(T, H, I, E, top_k, bm)
+    else:
+        nbytes = L.moe_fused_workspace_bytes(T, H, I, E, top_k, bm, int(w8a8 is not None))
     ws = _workspace(dev, ("fused", w8a8 is not None), nbytes)
     ids = torch.empty((T, top_k), dtype=torch.int32, device=dev) if return_routing else None
     wts = torch.empty((T, top_k), dtype=torch.float32, device=dev) if return_routing else None
     with torch.cuda.device(dev):
-        if w8a8 is None:
+        if router_weight is not None:
+            rc = L.moe_fused_forward_hidden(_ptr(x), _ptr(router_weight), _ptr(expert_bias), _ptr(w_gate),
+                                            _ptr(w_up), _ptr(w_down), _ptr(out), T, H, I, E, top_k, bm,
+                                            _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev))
+        elif w8a8 is None:
             rc = L.moe_fused_forward(_ptr(x), _ptr(router_logits), _ptr(expert_bias), _ptr(w_gate),
                                      _ptr(w_up), _ptr(w_down), _ptr(out), T, H, I, E, top_k, bm,
                                      _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev))

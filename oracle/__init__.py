@@ -12,6 +12,9 @@ Pinning (how each function is checked independently of its own formula):
 
 * ``route_topk``        -- brute-force rank counting + scipy softmax closed form
                            (tests/test_oracle_routing.py).
+* ``router_logits``     -- one-hot token rows select router-weight columns
+                           (catches a transposed operand) and a float64 numpy
+                           product (tests/test_oracle_routing.py).
 * ``align`` / ``metadata_from_group_sizes`` -- hand-written known answers
                            (problem_detail.json:40 example, RB:82-101 cases) and
                            permutation/padding invariants (tests/test_oracle_align.py).
@@ -28,6 +31,7 @@ Pinning (how each function is checked independently of its own formula):
 """
 
 from .moe_ref import (  # noqa: F401
+    router_logits,
     route_topk,
     align,
     metadata_from_group_sizes,

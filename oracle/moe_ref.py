@@ -14,6 +14,17 @@ LOG2E = 1.4426950408889634
 
 
 # ---------------------------------------------------------------------------
+# router GEMM (build-defined; the reference has no router, problem_detail.json
+# :18 and :30): logits = x . w_router^T with fp16 inputs and fp32 accumulation
+# ---------------------------------------------------------------------------
+def router_logits(x, w_router) -> np.ndarray:
+    """fp32 [T, E] logits of fp16 x [T, H] and w_router [E, H]."""
+    xf = _as_t(x).float()
+    wf = _as_t(w_router).float()
+    return (xf @ wf.t()).numpy().astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
 # routing: softmax -> top-k -> renormalise  (build-defined; the reference has no
 # router, problem_detail.json:18 and :30)
 # ---------------------------------------------------------------------------

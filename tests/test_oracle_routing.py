@@ -4,9 +4,10 @@ import itertools
 
 import numpy as np
 import pytest
+import torch
 from scipy.special import softmax
 
-from oracle import route_topk
+from oracle import route_topk, router_logits
 
 
 def _brute_topk(v, k):
@@ -76,3 +77,24 @@ def test_k_equals_one_weight_is_one(rng):
     ids, w = route_topk(logits, 1)
     assert (ids[:, 0] == logits.argmax(1)).all()
     np.testing.assert_array_equal(w, np.ones_like(w))
+
+
+def test_router_logits_one_hot_rows_select_weight_columns(rng):
+    """x = e_h (one-hot token rows) gives logits[:, e] = w_router[e, h]: a
+    transposed operand or a wrong contraction axis fails this."""
+    E, H = 5, 128
+    w = torch.from_numpy(rng.standard_normal((E, H)).astype(np.float16))
+    hs = [0, 7, 127]
+    x = torch.zeros((len(hs), H), dtype=torch.float16)
+    for t, h in enumerate(hs):
+        x[t, h] = 1.0
+    got = router_logits(x, w)
+    np.testing.assert_array_equal(got, w.float().numpy()[:, hs].T)
+
+
+def test_router_logits_against_float64(rng):
+    T, H, E = 9, 256, 12
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    w = (rng.standard_normal((E, H)) / 16).astype(np.float16)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    np.testing.assert_allclose(router_logits(torch.from_numpy(x), torch.from_numpy(w)), ref, rtol=1e-5, atol=1e-5)

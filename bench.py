@@ -153,6 +153,9 @@ def main():
     ap.add_argument("--router-gemm", action="store_true",
                     help="also time the router GEMM + routing (x . w_router^T, seeded w_router) alone and "
                          "the fused step started from hidden states (moe_fused_forward_hidden); fp16 only")
+    ap.add_argument("--shared-expert", action="store_true",
+                    help="also time the step with a DeepSeek-style always-on shared expert (seeded weights, "
+                         "moe_fused_forward_shared from the same logits) and check it on sampled tokens; fp16 only")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -284,6 +287,18 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
 
+    def timed(fn, fargs, label):
+        for _ in range(args.warmup):
+            check(fn(*fargs), label)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(args.steps):
+            check(fn(*fargs), label)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
+
     router = None
     if args.router_gemm and not w8:
         # router weight [E, H] ~ N(0, 1/H): logits ~ N(0, 1) like the configs' synthetic logits
@@ -298,19 +313,6 @@ def main():
                 [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + \
                 [P(out.data_ptr()), T, H, I, E, k, bm, P(hws.data_ptr()), hws.numel(), P(ids.data_ptr()),
                  P(wts.data_ptr()), stream]
-
-        def timed(fn, fargs, label):
-            for _ in range(args.warmup):
-                check(fn(*fargs), label)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            a.record()
-            for _ in range(args.steps):
-                check(fn(*fargs), label)
-            b.record()
-            torch.cuda.synchronize()
-            return a.elapsed_time(b) / args.steps
-
         r_ms = timed(L.moe_route_hidden, rargs, "moe_route_hidden")
         h_ms = timed(L.moe_fused_forward_hidden, hargs, "moe_fused_forward_hidden")
         r_flops = 2.0 * T * H * E
@@ -320,6 +322,38 @@ def main():
                   "router_roofline_frac": round(max(r_flops / (PEAK_F16_TFLOPS * 1e12),
                                                     r_bytes / (PEAK_HBM_GBS * 1e9)) / (r_ms * 1e-3), 4),
                   "fused_from_hidden_ms": round(h_ms, 4)}
+
+    shared = None
+    if args.shared_expert and not w8:
+        gs_ = torch.Generator(device=dev).manual_seed(SEED + 3)
+        sw = [torch.randn(shape, generator=gs_, device=dev, dtype=torch.float16) * 0.02
+              for shape in ((I, H), (I, H), (H, I))]
+        sbm = args.block_m or int(L.moe_pick_block_m(T, E + 1, k + 1))
+        sws = torch.empty(int(L.moe_fused_shared_workspace_bytes(T, H, I, E, k, sbm)), dtype=torch.uint8, device=dev)
+        sout = torch.empty_like(out)
+        sargs = head[:2] + [P(0), head[2]] + [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + \
+            [P(t.data_ptr()) for t in sw] + [P(sout.data_ptr()), T, H, I, E, k, sbm, P(sws.data_ptr()), sws.numel(),
+                                             P(0), P(0), stream]
+        s_ms = timed(L.moe_fused_forward_shared, sargs, "moe_fused_forward_shared")
+        b_ms = timed(fwd, cargs, name)  # routed-only step, timed the same way beside it
+        s_bytes = op_bytes + 3.0 * H * I * 2
+        s_flops = flops + 6.0 * H * I * T
+        shared = {"shared_ms": round(s_ms, 4), "routed_only_ms": round(b_ms, 4), "block_m": sbm,
+                  "extra_ms": round(s_ms - b_ms, 4),
+                  "gb_per_s": round(s_bytes / (s_ms * 1e-3) / 1e9, 1),
+                  "tflops": round(s_flops / (s_ms * 1e-3) / 1e12, 2),
+                  "frac_of_roofline_time": round(max(s_flops / (PEAK_F16_TFLOPS * 1e12),
+                                                     s_bytes / (PEAK_HBM_GBS * 1e9)) / (s_ms * 1e-3), 4)}
+        if not args.no_check:
+            from oracle import fused_moe_forward
+            rows = np.sort(np.random.default_rng(1).choice(T, min(T, 4), replace=False))
+            r = torch.from_numpy(rows).to(dev)
+            ref = fused_moe_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), inp["wg"], inp["wu"], inp["wd"], k,
+                                    None if inp["bias"] is None else inp["bias"].cpu(),
+                                    shared=[t.cpu() for t in sw]).float()
+            got = sout[r].float().cpu()
+            shared["within_rtol2e-2_atol1e-2"] = bool(torch.isfinite(got).all()) and \
+                bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
 
     copy_gbs = None
     if args.calib_copy:
@@ -388,6 +422,8 @@ def main():
         res["weight_quantisation_ms_once"] = round(quant_ms, 3)
     if router is not None:
         res["router"] = router
+    if shared is not None:
+        res["shared_expert"] = shared
     print(json.dumps(res), flush=True)
 
 

@@ -152,6 +152,27 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream);
 
+/* moe_fused_forward_shared: moe_fused_forward plus a DeepSeek-style always-on
+ * shared expert (w_gate_shared / w_up_shared fp16 [I, H], w_down_shared fp16
+ * [H, I]) run in the same Stage 1 / Stage 2 launches as the routed experts:
+ * every token takes it as choice k with weight 1 (not part of the top-k
+ * renormalisation), so out = routed MoE + SiLU(x.Wg_s^T) * (x.Wu_s^T) . Wd_s^T.
+ * Exactly one of logits (fp32 [T, E]) and w_router (fp16 [E, H], router GEMM
+ * as moe_route_hidden) is given.  topk_ids_out / topk_weights_out, when not
+ * null, are [T, k + 1] with column k = (E, 1.0).  Needs k + 1 <= 32 and
+ * E + 1 <= 1024; fp16 only; workspace moe_fused_shared_workspace_bytes bytes.
+ * No counterpart in the reference (problem_detail.json:18, :30: tokens go to
+ * routed experts only); DeepSeek-V3 layers add this expert beside them. */
+int64_t moe_fused_shared_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                         int64_t block_m);
+int moe_fused_forward_shared(const void* x, const float* logits, const void* w_router, const float* bias,
+                             const void* w_gate, const void* w_up, const void* w_down,
+                             const void* w_gate_shared, const void* w_up_shared,
+                             const void* w_down_shared, void* out, int64_t T, int64_t H, int64_t I,
+                             int64_t E, int64_t k, int64_t block_m, void* workspace,
+                             int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
+                             void* stream);
+
 /* ------------------------------------------------------------------------
  * W8A8.  moe_quantize_rows_w8: per-row symmetric int8 of an fp16 [R, K]
  * matrix: scale = max|row|/127, q = clamp(trunc(w*(127/max|row|) +- 0.5),

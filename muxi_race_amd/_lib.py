@@ -34,6 +34,9 @@ SIGNATURES = {
     "moe_fused_hidden_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "moe_fused_forward_hidden": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                         _p, _i64, _p, _p, _p]),
+    "moe_fused_shared_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "moe_fused_forward_shared": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                        _i64, _i64, _p, _i64, _p, _p, _p]),
     "moe_align": (_int, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "moe_fused_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _int]),
     "moe_pick_block_m": (_i64, [_i64, _i64, _i64]),

@@ -216,22 +216,31 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
   return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
 }
 
+// The always-on shared expert (wg_s / wu_s / wd_s non-null, fp16 only) runs as
+// expert E: every token takes it as choice k with weight 1, so the pipeline
+// works on E + 1 experts and k + 1 choices and the combine adds it last.
 static int fused_common(bool w8, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
-                        const void* wd, const float* sd, void* out, int64_t T, int64_t H,
+                        const void* wd, const float* sd, const void* wg_s, const void* wu_s,
+                        const void* wd_s, void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                         int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
                         void* const* ev) {
-  if (block_m == 0) block_m = pick_bm(T, E, k);
-  int rc = check_dims(T, H, I, E, k, block_m);
+  const bool shared = wg_s || wu_s || wd_s;
+  if (shared && (w8 || !wg_s || !wu_s || !wd_s))
+    return fail(w8 ? MOE_ERR_UNSUPPORTED : MOE_ERR_INVALID_ARG, w8 ? "the shared expert is supported on the fp16 path" : "null pointer argument");
+  const int64_t Ee = E + (shared ? 1 : 0), ke = k + (shared ? 1 : 0);  // experts / choices incl. the shared one
+  if (block_m == 0) block_m = pick_bm(T, Ee, ke);
+  int rc = check_dims(T, H, I, Ee, ke, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
   if (!x || (!logits && !w_router) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   if (w_router && (rc = check_router(x, w_router, T, H, E, k))) return rc;
-  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))))
+  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))) ||
+      (shared && (!aligned16(wg_s) || !aligned16(wu_s) || !aligned16(wd_s))))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
-  const FusedLayout L = fused_layout(T, H, I, E, k, block_m, w8);
+  const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, w8);
   const int64_t need = L.total + (w_router ? moe_router_workspace_bytes(T, H, E) : 0);
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
   hipStream_t s = (hipStream_t)stream;
@@ -242,19 +251,20 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   int32_t* gs = (int32_t*)(ws + L.gs);
   int32_t* go = (int32_t*)(ws + L.go);
   int32_t* gpo = (int32_t*)(ws + L.gpo);
-  const int64_t rows = cap_rows(T, k, E, block_m);
+  const int64_t rows = cap_rows(T, ke, Ee, block_m);
+  const int e_shared = shared ? (int)E : -1;
 
   // optional stage markers: ev[0] start, [1] routed, [2] aligned, [3] x quantised,
   // [4] stage 1, [5] stage 2, [6] combined
   auto mark = [&](int i) { if (ev && ev[i]) (void)hipEventRecord((hipEvent_t)ev[i], s); };
   mark(0);
   if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
-    if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s), "router"))) return rc;
-  } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s), "route_topk"))) {
+    if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s, e_shared), "router"))) return rc;
+  } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s, e_shared), "route_topk"))) {
     return rc;
   }
   mark(1);
-  if ((rc = check_launch(moe::launch_align(ids, (int)(T * k), (int)E, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
+  if ((rc = check_launch(moe::launch_align(ids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
   mark(2);
   if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, (int8_t*)(ws + L.xq), (float*)(ws + L.sx), s), "quantize_x"))) return rc;
   mark(3);
@@ -272,8 +282,11 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p1.gs = gs;
   p1.gpo = gpo;
   p1.sorted_ids = sorted;
-  p1.topk = (int)k;
-  p1.E = (int)E;
+  p1.wg_shared = (const char*)wg_s;
+  p1.wu_shared = (const char*)wu_s;
+  p1.e_shared = e_shared;
+  p1.topk = (int)ke;
+  p1.E = (int)Ee;
   p1.H = H;
   p1.I = I;
   if ((rc = check_launch(moe::launch_stage1(p1, (int)block_m, w8, true, rows / block_m, s), "stage1"))) return rc;
@@ -292,12 +305,14 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p2.go = go;
   p2.gpo = gpo;
   p2.sorted_ids = sorted;
-  p2.E = (int)E;
+  p2.wd_shared = (const char*)wd_s;
+  p2.e_shared = e_shared;
+  p2.E = (int)Ee;
   p2.H = H;
   p2.I = I;
   if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, w8, true, rows / block_m, s), "stage2"))) return rc;
   mark(5);
-  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)k, out, s), "combine");
+  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s), "combine");
   mark(6);
   return rc;
 }
@@ -307,7 +322,7 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias, con
                       int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                       int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                       void* stream) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -324,9 +339,29 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream) {
   if (!w_router && T > 0) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
+}
+
+int64_t moe_fused_shared_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                                         int64_t block_m) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  if (block_m == 0) block_m = pick_bm(T, E + 1, k + 1);
+  return fused_layout(T, H, I, E + 1, k + 1, block_m, false).total + moe_router_workspace_bytes(T, H, E);
+}
+
+int moe_fused_forward_shared(const void* x, const float* logits, const void* w_router, const float* bias,
+                             const void* w_gate, const void* w_up, const void* w_down, const void* w_gate_shared,
+                             const void* w_up_shared, const void* w_down_shared, void* out, int64_t T,
+                             int64_t H, int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
+                             int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
+                             void* stream) {
+  if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
+  if (T > 0 && (!w_gate_shared || !w_up_shared || !w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return fused_common(false, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
+                      w_gate_shared, w_up_shared, w_down_shared, out, T, H, I, E, k, block_m, workspace,
+                      workspace_bytes, topk_ids_out, topk_weights_out, stream, nullptr);
 }
 
 int moe_fused_forward_events(const void* x, const float* logits, const float* bias,
@@ -335,7 +370,7 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }
@@ -355,7 +390,7 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                            void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                            int64_t block_m, void* workspace, int64_t workspace_bytes,
                            int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -367,7 +402,7 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int64_t block_m, void* workspace, int64_t workspace_bytes,
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }

@@ -82,6 +82,10 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
+  // this expert's [I, H] gate / up weights (the shared expert's own tensors)
+  const bool sh = p.e_shared >= 0 && e == p.e_shared;
+  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.I * kbytes;
+  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.I * kbytes;
 
   LD ld;
 #pragma unroll
@@ -98,9 +102,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       }
       src = p.x + src_row * kbytes;
     } else if (r < rx + rw) {
-      src = p.wg + ((int64_t)e * p.I + n0 + (r - rx)) * kbytes;
+      src = gexp + (int64_t)(n0 + r - rx) * kbytes;
     } else {
-      src = p.wu + ((int64_t)e * p.I + n0 + (r - rx - rw)) * kbytes;
+      src = uexp + (int64_t)(n0 + r - rx - rw) * kbytes;
     }
     ld.set(i, src);
   }
@@ -295,6 +299,9 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
 
   const int64_t kbytes = p.H * 2;
   const int nk = (int)(kbytes / kRowBytes);
+  const bool sh = p.e_shared >= 0 && e == p.e_shared;  // see stage1_kernel
+  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.I * kbytes;
+  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.I * kbytes;
   LD ld;
 #pragma unroll
   for (int i = 0; i < LD::NI; ++i) {
@@ -304,9 +311,9 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
       const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
       src = p.x + (int64_t)(pid / p.topk) * kbytes;
     } else if (r < BM + BN) {
-      src = p.wg + ((int64_t)e * p.I + n0 + (r - BM)) * kbytes;
+      src = gexp + (int64_t)(n0 + r - BM) * kbytes;
     } else {
-      src = p.wu + ((int64_t)e * p.I + n0 + (r - BM - BN)) * kbytes;
+      src = uexp + (int64_t)(n0 + r - BM - BN) * kbytes;
     }
     ld.set(i, src);
   }
@@ -427,12 +434,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
+  // this expert's [H, I] down weights (the shared expert's own tensor)
+  const char* dexp = p.e_shared >= 0 && e == p.e_shared ? p.wd_shared : p.wd + (int64_t)e * p.H * kbytes;
   LD ld;
 #pragma unroll
   for (int i = 0; i < LD::NI; ++i) {
     const int r = LD::row_of(i);
-    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * kbytes
-                     : p.wd + ((int64_t)e * p.H + n0 + (r - rx)) * kbytes);
+    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * kbytes : dexp + (int64_t)(n0 + r - rx) * kbytes);
   }
 
   const int wave = threadIdx.x >> 6;

@@ -20,6 +20,9 @@ struct Stage1Params {
   const int32_t* gs;        // [E]
   const int32_t* gpo;       // [E+1]
   const int32_t* sorted_ids;  // gather only: [padded rows], sentinel = T*topk
+  const char* wg_shared;    // weights of expert e_shared ([I, H]) when e_shared >= 0
+  const char* wu_shared;
+  int e_shared = -1;        // always-on shared expert's index, or -1
   int topk;
   int E;
   int64_t H;
@@ -41,6 +44,8 @@ struct Stage2Params {
   const int32_t* go;
   const int32_t* gpo;
   const int32_t* sorted_ids;  // fused only
+  const char* wd_shared;    // down weights of expert e_shared ([H, I]) when e_shared >= 0
+  int e_shared = -1;        // always-on shared expert's index, or -1
   int E;
   int64_t H;
   int64_t I;
@@ -53,8 +58,10 @@ hipError_t launch_stage1(const Stage1Params& p, int block_m, bool int8, bool gat
 hipError_t launch_stage2(const Stage2Params& p, int block_m, bool int8, bool fused,
                          int64_t max_blocks, hipStream_t stream);
 
+// With e_shared >= 0 every token also gets the shared expert as choice k
+// (id e_shared, weight 1): ids / w rows hold k + 1 entries.
 hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
-                             int32_t* ids, float* w, hipStream_t stream);
+                             int32_t* ids, float* w, hipStream_t stream, int e_shared = -1);
 // `whist` (int32 [align_groups(P) * E], may be null) lets a large P be aligned
 // by align_groups(P) workgroups in two launches instead of one workgroup.
 constexpr int kAlignPairsPerGroup = 2048;
@@ -78,7 +85,8 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int block_m, int32_t* 
 int router_splits(int64_t T, int64_t H, int64_t E);
 int64_t router_partial_floats(int64_t T, int64_t H, int64_t E);
 hipError_t launch_router(const void* x, const void* w_router, const float* bias, int T, int64_t H, int E,
-                         int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t stream);
+                         int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t stream,
+                         int e_shared = -1);
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream);
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,

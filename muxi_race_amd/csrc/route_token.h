@@ -21,10 +21,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Routes token t; logit(e) returns its logit for expert e (lane l asks for
-// experts l, l + 64, ...).  Lane j < k writes choice j.
+// experts l, l + 64, ...).  Lane j < k writes choice j to ids / wout at
+// t * kout + j; with e_shared >= 0, lane k appends the always-on shared
+// expert (id e_shared, weight 1) as choice k (kout = k + 1).
 template <int VPL, typename Logit>
 __device__ __forceinline__ void route_token_with(Logit&& logit, const float* __restrict__ bias, int t, int E,
-                                                 int k, int32_t* __restrict__ ids, float* __restrict__ wout) {
+                                                 int k, int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                 int kout = 0, int e_shared = -1) {
+  if (kout == 0) kout = k;
   const int l = lane_id();
   float v[VPL];
   uint32_t valid = 0;
@@ -83,8 +87,11 @@ __device__ __forceinline__ void route_token_with(Logit&& logit, const float* __r
     }
   }
   if (l < k) {
-    ids[(int64_t)t * k + l] = my_id;
-    wout[(int64_t)t * k + l] = my_p / denom;
+    ids[(int64_t)t * kout + l] = my_id;
+    wout[(int64_t)t * kout + l] = my_p / denom;
+  } else if (l == k && e_shared >= 0) {
+    ids[(int64_t)t * kout + k] = e_shared;
+    wout[(int64_t)t * kout + k] = 1.0f;
   }
 }
 

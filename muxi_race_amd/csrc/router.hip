@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void route_partials_kernel(const float* __rest
                                                              const float* __restrict__ bias, int T, int E,
                                                              int k, int32_t* __restrict__ ids,
                                                              float* __restrict__ wout,
-                                                             float* __restrict__ logits) {
+                                                             float* __restrict__ logits, int e_shared) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // uniform per wave
   // partials loaded 8 at a time (independent loads in flight), summed in split order
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void route_partials_kernel(const float* __rest
     if (logits) logits[(int64_t)t * E + e] = v;
     return v;
   };
-  route_token_with<VPL>(logit, bias, t, E, k, ids, wout);
+  route_token_with<VPL>(logit, bias, t, E, k, ids, wout, e_shared >= 0 ? k + 1 : k, e_shared);
 }
 
 // Tile of the router GEMM: 128 tokens x MOE_ROUTER_BN experts (8 waves) when
@@ -168,7 +168,8 @@ int router_splits(int64_t T, int64_t H, int64_t E) {
 int64_t router_partial_floats(int64_t T, int64_t H, int64_t E) { return router_splits(T, H, E) * T * E; }
 
 hipError_t launch_router(const void* x, const void* w_router, const float* bias, int T, int64_t H, int E,
-                         int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t s) {
+                         int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t s,
+                         int e_shared) {
   if (T == 0) return hipSuccess;
   const int ks = router_splits(T, H, E);
   const int64_t grid = router_items(T, E) * ks;
@@ -184,7 +185,8 @@ hipError_t launch_router(const void* x, const void* w_router, const float* bias,
   if (err != hipSuccess) return err;
   const dim3 rgrid((T + 3) / 4), block(256);
   const int vpl = (E + 63) / 64;
-#define MOE_RP(V) hipLaunchKernelGGL((route_partials_kernel<V>), rgrid, block, 0, s, part, ks, bias, T, E, k, ids, w, logits)
+#define MOE_RP(V) hipLaunchKernelGGL((route_partials_kernel<V>), rgrid, block, 0, s, part, ks, bias, T, E, k, ids, w, logits, \
+                                     e_shared)
   if (vpl <= 1) MOE_RP(1);
   else if (vpl <= 2) MOE_RP(2);
   else if (vpl <= 4) MOE_RP(4);

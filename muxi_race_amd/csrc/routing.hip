@@ -15,23 +15,26 @@ template <int VPL>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          const float* __restrict__ bias, int T,
                                                          int E, int k, int32_t* __restrict__ ids,
-                                                         float* __restrict__ wout) {
+                                                         float* __restrict__ wout, int e_shared) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // uniform per wave
   const float* row = logits + (int64_t)t * E;
-  route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout);
+  route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout,
+                        e_shared >= 0 ? k + 1 : k, e_shared);
 }
 
 hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
-                             int32_t* ids, float* w, hipStream_t s) {
+                             int32_t* ids, float* w, hipStream_t s, int e_shared) {
   if (T == 0) return hipSuccess;
   const dim3 grid((T + 3) / 4), block(256);
   const int vpl = (E + 63) / 64;
-  if (vpl <= 1) hipLaunchKernelGGL(route_topk_kernel<1>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
-  else if (vpl <= 2) hipLaunchKernelGGL(route_topk_kernel<2>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
-  else if (vpl <= 4) hipLaunchKernelGGL(route_topk_kernel<4>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
-  else if (vpl <= 8) hipLaunchKernelGGL(route_topk_kernel<8>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
-  else hipLaunchKernelGGL(route_topk_kernel<16>, grid, block, 0, s, logits, bias, T, E, k, ids, w);
+#define MOE_RT(V) hipLaunchKernelGGL(route_topk_kernel<V>, grid, block, 0, s, logits, bias, T, E, k, ids, w, e_shared)
+  if (vpl <= 1) MOE_RT(1);
+  else if (vpl <= 2) MOE_RT(2);
+  else if (vpl <= 4) MOE_RT(4);
+  else if (vpl <= 8) MOE_RT(8);
+  else MOE_RT(16);
+#undef MOE_RT
   return hipGetLastError();
 }
 

@@ -238,13 +238,16 @@ def quantize_w8a8_weights(w_gate, w_up, w_down) -> W8A8Weights:
 # ---------------------------------------------------------------------------
 def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
               expert_bias=None, w8a8: W8A8Weights | None = None, block_m: int = 0, out=None,
-              return_routing: bool = False, router_weight=None):
+              return_routing: bool = False, router_weight=None, shared_expert=None):
     """Full MoE FFN: softmax/top-k/renormalise routing, expert SwiGLU MLPs,
     routing-weighted combine.  hidden_states fp16 [T, H], router_logits fp32
     [T, E], w_gate/w_up fp16 [E, I, H], w_down fp16 [E, H, I] (or ``w8a8``
     quantised weights, in which case w_gate/w_up/w_down may be None).
     With ``router_weight`` (fp16 [E, H]) and router_logits None (fp16 path
     only), the logits are computed in the same call by the router GEMM.
+    ``shared_expert`` = (w_gate_s [I, H], w_up_s [I, H], w_down_s [H, I]) fp16
+    adds an always-on expert with weight 1 in the same launches (fp16 path);
+    the returned routing then has k + 1 columns, the last being (E, 1.0).
     Returns fp16 [T, H] (and (ids, weights) when ``return_routing``)."""
     x = hidden_states
     _need(x, "hidden_states", (torch.float16,), 2)
@@ -283,6 +286,16 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
                 tuple(q.q_down.shape) != (E, H, I) or tuple(q.s_gate.shape) != (E, I) or \
                 tuple(q.s_up.shape) != (E, I) or tuple(q.s_down.shape) != (E, H):
             raise ValueError("W8A8 weight/scale shapes do not match")
+    if shared_expert is not None:
+        if w8a8 is not None:
+            raise ValueError("shared_expert is supported on the fp16 path")
+        if len(shared_expert) != 3:
+            raise ValueError("shared_expert is (w_gate, w_up, w_down)")
+        for name, t in zip(("w_gate_shared", "w_up_shared", "w_down_shared"), shared_expert):
+            _need(t, name, (torch.float16,), 2, dev)
+        sg_, su_, sd_ = shared_expert
+        if tuple(sg_.shape) != (I, H) or tuple(su_.shape) != (I, H) or tuple(sd_.shape) != (H, I):
+            raise ValueError("shared expert shapes do not match [I,H]/[I,H]/[H,I]")
     if expert_bias is not None:
         _need(expert_bias, "expert_bias", (torch.float32,), 1, dev)
         if expert_bias.numel() != E:
@@ -294,16 +307,24 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
         if tuple(out.shape) != (T, H):
             raise ValueError("out shape mismatch")
     L = lib()
-    bm = block_m or int(L.moe_pick_block_m(T, E, top_k))
-    if router_weight is not None:
+    ncol = top_k + (shared_expert is not None)
+    bm = block_m or int(L.moe_pick_block_m(T, E + (shared_expert is not None), ncol))
+    if shared_expert is not None:
+        nbytes = L.moe_fused_shared_workspace_bytes(T, H, I, E, top_k, bm)
+    elif router_weight is not None:
         nbytes = L.moe_fused_hidden_workspace_bytes(T, H, I, E, top_k, bm)
     else:
         nbytes = L.moe_fused_workspace_bytes(T, H, I, E, top_k, bm, int(w8a8 is not None))
     ws = _workspace(dev, ("fused", w8a8 is not None), nbytes)
-    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev) if return_routing else None
-    wts = torch.empty((T, top_k), dtype=torch.float32, device=dev) if return_routing else None
+    ids = torch.empty((T, ncol), dtype=torch.int32, device=dev) if return_routing else None
+    wts = torch.empty((T, ncol), dtype=torch.float32, device=dev) if return_routing else None
     with torch.cuda.device(dev):
-        if router_weight is not None:
+        if shared_expert is not None:
+            rc = L.moe_fused_forward_shared(
+                _ptr(x), _ptr(router_logits), _ptr(router_weight), _ptr(expert_bias), _ptr(w_gate), _ptr(w_up),
+                _ptr(w_down), _ptr(sg_), _ptr(su_), _ptr(sd_), _ptr(out), T, H, I, E, top_k, bm, _ptr(ws),
+                ws.numel(), _ptr(ids), _ptr(wts), _stream(dev))
+        elif router_weight is not None:
             rc = L.moe_fused_forward_hidden(_ptr(x), _ptr(router_weight), _ptr(expert_bias), _ptr(w_gate),
                                             _ptr(w_up), _ptr(w_down), _ptr(out), T, H, I, E, top_k, bm,
                                             _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev))

@@ -189,19 +189,30 @@ def combine(y_pair: torch.Tensor, T: int, top_k: int) -> torch.Tensor:
 
 
 def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
-                      block_m: int = 128, *, return_aux=False, experts=None):
+                      block_m: int = 128, *, return_aux=False, experts=None, shared=None):
     """Full MoE: route -> align -> gather -> pre-routed MLP -> weighted combine.
 
     Returns float16 [T, H] (and the routing/alignment intermediates when
     ``return_aux``).  The pre-routed step is exactly ``prerouted_forward`` with
     routed weights taken in sorted-pair order, so the expert math is the
-    reference's own loop.
+    reference's own loop.  ``shared`` = (w_gate_s [I, H], w_up_s [I, H],
+    w_down_s [H, I]) adds an always-on expert: expert E, appended to every
+    token as choice k with weight 1 (outside the top-k renormalisation), so
+    the routing has k + 1 columns.
     """
     x = _as_t(x)
     T, H = x.shape
     E = int(w_gate.shape[0])
     ids, w = route_topk(_as_t(logits).float().numpy(), top_k,
                         None if bias is None else _as_t(bias).float().numpy())
+    if shared is not None:
+        ids = np.concatenate([ids, np.full((T, 1), E, np.int32)], axis=1)
+        w = np.concatenate([w, np.ones((T, 1), np.float32)], axis=1)
+        sg, su, sd = (_as_t(a) for a in shared)
+        w_gate = torch.cat([_as_t(w_gate), sg[None]])
+        w_up = torch.cat([_as_t(w_up), su[None]])
+        w_down = torch.cat([_as_t(w_down), sd[None]])
+        E, top_k = E + 1, top_k + 1
     al = align(ids, E, block_m)
     sp = al["sorted_pair_ids"]
     P = T * top_k

@@ -61,6 +61,17 @@ def test_host_validation_without_gpu():
     assert rc == -2 and b"block_m" in L.moe_last_error_string()
     rc = L.moe_quantize_rows_w8(nul, 4, 12, nul, nul, nul)
     assert rc == -1
+    # shared expert: exactly one of logits / w_router, and k + 1 <= 32
+    one = ctypes.c_void_p(256)
+    rc = L.moe_fused_forward_shared(nul, one, one, nul, nul, nul, nul, one, one, one, nul, 4, 128, 128, 64, 2,
+                                    0, nul, 0, nul, nul, nul)
+    assert rc == -1 and b"exactly one" in L.moe_last_error_string()
+    rc = L.moe_fused_forward_shared(nul, one, nul, nul, nul, nul, nul, one, one, one, nul, 4, 128, 128, 64, 32,
+                                    0, nul, 0, nul, nul, nul)
+    assert rc == -2 and b"top_k" in L.moe_last_error_string()
+    rc = L.moe_fused_forward_shared(nul, one, nul, nul, nul, nul, nul, one, nul, one, nul, 4, 128, 128, 64, 2,
+                                    0, nul, 0, nul, nul, nul)
+    assert rc == -1
 
 
 def test_capacity_and_workspace_sizes():
@@ -74,3 +85,7 @@ def test_capacity_and_workspace_sizes():
     assert L.moe_pick_block_m(32, 256, 8) == 32
     ws = L.moe_fused_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 0)
     assert ws >= 32768 * 7168 * 2 + 65280 * 2048 * 2
+    # the shared expert is expert E, choice k: the fused layout for (E + 1, k + 1)
+    # plus the router's partial sums
+    assert L.moe_fused_shared_workspace_bytes(4096, 7168, 2048, 256, 8, 128) == \
+        L.moe_fused_workspace_bytes(4096, 7168, 2048, 257, 9, 128, 0) + L.moe_router_workspace_bytes(4096, 7168, 256)

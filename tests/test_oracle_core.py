@@ -179,3 +179,36 @@ def test_fused_matches_dense_per_token(rng):
                 u = wu[e].double() @ xt
                 exp[t] += float(w[t, j]) * (wd[e].double() @ (torch.sigmoid(g) * g * u))
         torch.testing.assert_close(out.double(), exp, rtol=2e-3, atol=2e-3)
+
+
+def test_shared_expert_closed_forms(rng):
+    """Shared expert: (1) with k = 1 and every token routed to expert 0, a
+    shared expert equal to expert 0 doubles the output exactly (both terms have
+    weight 1, fp32 sums, and fp16 scaling by 2 is exact); (2) the shared
+    output minus the routed-only output is the dense SwiGLU MLP of x with the
+    shared weights, computed per token in fp64 without routing or sorting."""
+    T, H, I, E = 37, 32, 16, 5
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16))
+    wg = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wu = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wd = torch.from_numpy((rng.standard_normal((E, H, I)) * 0.2).astype(np.float16))
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    hot = logits.clone()
+    hot[:, 0] += 100.0
+    base, aux = fused_moe_forward(x, hot, wg, wu, wd, 1, return_aux=True)
+    assert (aux["ids"][:, 0] == 0).all()
+    doubled, aux2 = fused_moe_forward(x, hot, wg, wu, wd, 1, shared=(wg[0], wu[0], wd[0]), return_aux=True)
+    assert torch.equal(doubled, base * 2)
+    np.testing.assert_array_equal(aux2["ids"][:, 1], np.full(T, E))
+    np.testing.assert_array_equal(aux2["weights"][:, 1], np.ones(T, np.float32))
+
+    sg = torch.from_numpy((rng.standard_normal((I, H)) * 0.2).astype(np.float16))
+    su = torch.from_numpy((rng.standard_normal((I, H)) * 0.2).astype(np.float16))
+    sd = torch.from_numpy((rng.standard_normal((H, I)) * 0.2).astype(np.float16))
+    for k, bm in ((2, 32), (3, 128)):
+        routed = fused_moe_forward(x, logits, wg, wu, wd, k, block_m=bm)
+        both = fused_moe_forward(x, logits, wg, wu, wd, k, block_m=bm, shared=(sg, su, sd))
+        xd = x.double()
+        g, u = xd @ sg.double().T, xd @ su.double().T
+        dense = (torch.sigmoid(g) * g * u) @ sd.double().T
+        torch.testing.assert_close(both.double() - routed.double(), dense, rtol=2e-3, atol=3e-3)

@@ -153,6 +153,9 @@ def main():
     ap.add_argument("--router-gemm", action="store_true",
                     help="also time the router GEMM + routing (x . w_router^T, seeded w_router) alone and "
                          "the fused step started from hidden states (moe_fused_forward_hidden); fp16 only")
+    ap.add_argument("--weights", choices=("dense", "w13"), default="dense",
+                    help="fp16 weight layout: dense [E, N, K] tensors, or gate and up as the two halves of "
+                         "one fused [E, 2I, H] tensor (built once, before timing; moe_fused_forward_ex)")
     ap.add_argument("--shared-expert", action="store_true",
                     help="also time the step with a DeepSeek-style always-on shared expert (seeded weights, "
                          "moe_fused_forward_shared from the same logits) and check it on sampled tokens; fp16 only")
@@ -200,6 +203,13 @@ def main():
         cargs = head + [P(t.data_ptr()) for t in (qw.q_gate, qw.s_gate, qw.q_up, qw.s_up, qw.q_down,
                                                    qw.s_down)] + tail
         fwd, fwd_ev, name = L.moe_fused_forward_w8a8, L.moe_fused_forward_w8a8_events, "moe_fused_forward_w8a8"
+    elif args.weights == "w13":
+        w13 = torch.cat([inp["wg"], inp["wu"]], dim=1)  # [E, 2I, H]
+        wstr = (ctypes.c_int64 * 4)(H, 2 * I * H, 0, 0)
+        cargs = head[:2] + [P(0), head[2]] + [P(w13[:, :I].data_ptr()), P(w13[:, I:].data_ptr()),
+                                              P(inp["wd"].data_ptr())] + [P(0), P(0), P(0), wstr] + tail
+        fwd = lambda *a: L.moe_fused_forward_ex(*a, P(0))
+        fwd_ev, name = L.moe_fused_forward_ex, "moe_fused_forward_ex"
     else:
         cargs = head + [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + tail
         fwd, fwd_ev, name = L.moe_fused_forward, L.moe_fused_forward_events, "moe_fused_forward"
@@ -390,7 +400,8 @@ def main():
         "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} "
                                + ("W8A8 int8" if w8 else "fp16"),
                    "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
-                   "block_m": bm, "experts_touched": int(touched)},
+                   "block_m": bm, "experts_touched": int(touched),
+                   "weight_layout": "int8 dense" if w8 else args.weights},
         "gb_per_s": round(gbs, 1),
         "frac_mfma_peak": round(tflops / peak_c, 4),
         "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),

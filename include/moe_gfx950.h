@@ -173,6 +173,29 @@ int moe_fused_forward_shared(const void* x, const float* logits, const void* w_r
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream);
 
+/* moe_fused_forward_ex: the general fp16 entry -- logits or w_router (exactly
+ * one), the shared expert optional (all three pointers or none), and strided
+ * weights.  weight_strides (host int64_t[4], or NULL for dense weights) holds,
+ * in elements, {row stride, expert stride} of w_gate and w_up, then of w_down,
+ * 0 meaning dense: row n of expert e of w_gate starts at element
+ * e * s[1] + n * s[0], of w_down at e * s[3] + n * s[2].  Rows must not
+ * overlap (s[0] >= H, s[1] >= I * s[0], s[2] >= I, s[3] >= H * s[2]) and stay
+ * 16-byte aligned (multiples of 8).  This takes, without a copy, gate and up as
+ * the two halves of a fused [E, 2I, H] tensor (expert stride 2*I*H).  The
+ * shared expert's matrices use the same row strides.  stage_events as for
+ * moe_fused_forward_events, or NULL.  Workspace:
+ * moe_fused_ex_workspace_bytes(..., shared, with_router).  No counterpart in
+ * the reference (its run_kernel takes dense weights, problem_detail.json:24). */
+int64_t moe_fused_ex_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t block_m,
+                                     int shared, int with_router);
+int moe_fused_forward_ex(const void* x, const float* logits, const void* w_router, const float* bias,
+                         const void* w_gate, const void* w_up, const void* w_down,
+                         const void* w_gate_shared, const void* w_up_shared, const void* w_down_shared,
+                         const int64_t* weight_strides, void* out, int64_t T, int64_t H, int64_t I,
+                         int64_t E, int64_t k, int64_t block_m, void* workspace, int64_t workspace_bytes,
+                         int32_t* topk_ids_out, float* topk_weights_out, void* stream,
+                         void* const* stage_events);
+
 /* ------------------------------------------------------------------------
  * W8A8.  moe_quantize_rows_w8: per-row symmetric int8 of an fp16 [R, K]
  * matrix: scale = max|row|/127, q = clamp(trunc(w*(127/max|row|) +- 0.5),

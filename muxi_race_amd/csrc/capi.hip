@@ -222,7 +222,7 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
 static int fused_common(bool w8, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
                         const void* wd, const float* sd, const void* wg_s, const void* wu_s,
-                        const void* wd_s, void* out, int64_t T, int64_t H,
+                        const void* wd_s, const int64_t* wstr, void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                         int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
                         void* const* ev) {
@@ -237,6 +237,17 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   if (!x || (!logits && !w_router) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   if (w_router && (rc = check_router(x, w_router, T, H, E, k))) return rc;
+  // weight strides in elements, {row, expert} of gate/up then of down (null
+  // or 0: dense); rows must not overlap and stay 16-byte aligned
+  const int64_t eb = w8 ? 1 : 2;
+  int64_t ld_gu = wstr ? wstr[0] : 0, es_gu = wstr ? wstr[1] : 0, ld_d = wstr ? wstr[2] : 0, es_d = wstr ? wstr[3] : 0;
+  ld_gu = ld_gu ? ld_gu : H;
+  ld_d = ld_d ? ld_d : I;
+  es_gu = es_gu ? es_gu : I * ld_gu;
+  es_d = es_d ? es_d : H * ld_d;
+  if (ld_gu < H || ld_d < I || es_gu < I * ld_gu || es_d < H * ld_d || (ld_gu | es_gu | ld_d | es_d) * eb % 16)
+    return fail(MOE_ERR_INVALID_ARG, "weight strides (rows %lld / %lld, experts %lld / %lld) must not overlap rows and must keep 16-byte alignment",
+                (long long)ld_gu, (long long)ld_d, (long long)es_gu, (long long)es_d);
   if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))) ||
       (shared && (!aligned16(wg_s) || !aligned16(wu_s) || !aligned16(wd_s))))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
@@ -285,6 +296,8 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p1.wg_shared = (const char*)wg_s;
   p1.wu_shared = (const char*)wu_s;
   p1.e_shared = e_shared;
+  p1.w_ld = ld_gu * eb;
+  p1.w_es = es_gu * eb;
   p1.topk = (int)ke;
   p1.E = (int)Ee;
   p1.H = H;
@@ -307,6 +320,8 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p2.sorted_ids = sorted;
   p2.wd_shared = (const char*)wd_s;
   p2.e_shared = e_shared;
+  p2.wd_ld = ld_d * eb;
+  p2.wd_es = es_d * eb;
   p2.E = (int)Ee;
   p2.H = H;
   p2.I = I;
@@ -322,7 +337,7 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias, con
                       int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                       int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                       void* stream) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -339,7 +354,7 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream) {
   if (!w_router && T > 0) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -360,8 +375,30 @@ int moe_fused_forward_shared(const void* x, const float* logits, const void* w_r
   if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
   if (T > 0 && (!w_gate_shared || !w_up_shared || !w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   return fused_common(false, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
-                      w_gate_shared, w_up_shared, w_down_shared, out, T, H, I, E, k, block_m, workspace,
+                      w_gate_shared, w_up_shared, w_down_shared, nullptr, out, T, H, I, E, k, block_m, workspace,
                       workspace_bytes, topk_ids_out, topk_weights_out, stream, nullptr);
+}
+
+int64_t moe_fused_ex_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t block_m,
+                                     int shared, int with_router) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  const int64_t s = shared ? 1 : 0;
+  if (block_m == 0) block_m = pick_bm(T, E + s, k + s);
+  return fused_layout(T, H, I, E + s, k + s, block_m, false).total + (with_router ? moe_router_workspace_bytes(T, H, E) : 0);
+}
+
+int moe_fused_forward_ex(const void* x, const float* logits, const void* w_router, const float* bias,
+                         const void* w_gate, const void* w_up, const void* w_down, const void* w_gate_shared,
+                         const void* w_up_shared, const void* w_down_shared, const int64_t* weight_strides,
+                         void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t block_m,
+                         void* workspace, int64_t workspace_bytes, int32_t* topk_ids_out,
+                         float* topk_weights_out, void* stream, void* const* stage_events) {
+  if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
+  const bool any = w_gate_shared || w_up_shared || w_down_shared;
+  if (T > 0 && any && !(w_gate_shared && w_up_shared && w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return fused_common(false, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
+                      w_gate_shared, w_up_shared, w_down_shared, weight_strides, out, T, H, I, E, k, block_m,
+                      workspace, workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
 }
 
 int moe_fused_forward_events(const void* x, const float* logits, const float* bias,
@@ -370,7 +407,7 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }
@@ -390,7 +427,7 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                            void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                            int64_t block_m, void* workspace, int64_t workspace_bytes,
                            int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -402,7 +439,7 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int64_t block_m, void* workspace, int64_t workspace_bytes,
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, out,
+  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }

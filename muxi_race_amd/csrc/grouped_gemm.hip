@@ -82,10 +82,11 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
-  // this expert's [I, H] gate / up weights (the shared expert's own tensors)
+  // this expert's [I, H] gate / up weights, experts w_es and rows w_ld bytes
+  // apart (the shared expert's own tensors, same row stride)
   const bool sh = p.e_shared >= 0 && e == p.e_shared;
-  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.I * kbytes;
-  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.I * kbytes;
+  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.w_es;
+  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.w_es;
 
   LD ld;
 #pragma unroll
@@ -102,9 +103,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       }
       src = p.x + src_row * kbytes;
     } else if (r < rx + rw) {
-      src = gexp + (int64_t)(n0 + r - rx) * kbytes;
+      src = gexp + (int64_t)(n0 + r - rx) * p.w_ld;
     } else {
-      src = uexp + (int64_t)(n0 + r - rx - rw) * kbytes;
+      src = uexp + (int64_t)(n0 + r - rx - rw) * p.w_ld;
     }
     ld.set(i, src);
   }
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     for (int b = 0; b < L::NBM; ++b) {
       const int m = xr0 + 32 * b + (l & 31);
       if (m < actual) {
-        _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.I;
+        _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.h_ld;
 #pragma unroll
         for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
       if (mrow < actual) {
         const int64_t grow = row0 + mrow;
-        int8_t* hrow = reinterpret_cast<int8_t*>(p.h) + grow * p.I;
+        int8_t* hrow = reinterpret_cast<int8_t*>(p.h) + grow * p.h_ld;
 #pragma unroll
         for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
@@ -300,8 +301,8 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
   const int64_t kbytes = p.H * 2;
   const int nk = (int)(kbytes / kRowBytes);
   const bool sh = p.e_shared >= 0 && e == p.e_shared;  // see stage1_kernel
-  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.I * kbytes;
-  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.I * kbytes;
+  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.w_es;
+  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.w_es;
   LD ld;
 #pragma unroll
   for (int i = 0; i < LD::NI; ++i) {
@@ -311,9 +312,9 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
       const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
       src = p.x + (int64_t)(pid / p.topk) * kbytes;
     } else if (r < BM + BN) {
-      src = gexp + (int64_t)(n0 + r - BM) * kbytes;
+      src = gexp + (int64_t)(n0 + r - BM) * p.w_ld;
     } else {
-      src = uexp + (int64_t)(n0 + r - BM - BN) * kbytes;
+      src = uexp + (int64_t)(n0 + r - BM - BN) * p.w_ld;
     }
     ld.set(i, src);
   }
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
   if (writer) {
     const int m = l & 31;
     if (m < actual) {
-      _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.I;
+      _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.h_ld;
       const int fbase = KSPLIT ? 0 : 32 * half;
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
@@ -434,13 +435,15 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 
   const int64_t kbytes = p.I * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);
-  // this expert's [H, I] down weights (the shared expert's own tensor)
-  const char* dexp = p.e_shared >= 0 && e == p.e_shared ? p.wd_shared : p.wd + (int64_t)e * p.H * kbytes;
+  // this expert's [H, I] down weights, experts wd_es and rows wd_ld bytes
+  // apart (the shared expert's own tensor, same row stride); intermediate rows
+  // a_ld bytes apart
+  const char* dexp = p.e_shared >= 0 && e == p.e_shared ? p.wd_shared : p.wd + (int64_t)e * p.wd_es;
   LD ld;
 #pragma unroll
   for (int i = 0; i < LD::NI; ++i) {
     const int r = LD::row_of(i);
-    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * kbytes : dexp + (int64_t)(n0 + r - rx) * kbytes);
+    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * p.a_ld : dexp + (int64_t)(n0 + r - rx) * p.wd_ld);
   }
 
   const int wave = threadIdx.x >> 6;
@@ -671,6 +674,9 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, boo
                          int64_t max_blocks, hipStream_t s) {
   Stage1Params p = params;
   p.host_blocks = (int)max_blocks;
+  if (p.w_ld == 0) p.w_ld = p.H * (int8 ? 1 : 2);
+  if (p.w_es == 0) p.w_es = p.I * p.w_ld;
+  if (p.h_ld == 0) p.h_ld = p.I;
   const int64_t grid = schedule_grid(max_blocks, p.I / kBN);
   if (grid <= 0) return hipSuccess;
   constexpr int NW = MOE_S1_WAVES_128;
@@ -701,6 +707,9 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, bool int8, boo
                          int64_t max_blocks, hipStream_t s) {
   Stage2Params p = params;
   p.host_blocks = (int)max_blocks;
+  if (p.a_ld == 0) p.a_ld = p.I * (int8 ? 1 : 2);
+  if (p.wd_ld == 0) p.wd_ld = p.I * (int8 ? 1 : 2);
+  if (p.wd_es == 0) p.wd_es = p.H * p.wd_ld;
   const int64_t mb = max_blocks;
   if (!fused) {
     if (block_m == 128 && !int8) return go2_128<false, false>(p, mb, s);

@@ -23,6 +23,9 @@ struct Stage1Params {
   const char* wg_shared;    // weights of expert e_shared ([I, H]) when e_shared >= 0
   const char* wu_shared;
   int e_shared = -1;        // always-on shared expert's index, or -1
+  int64_t w_ld = 0;         // bytes between rows of wg / wu / the shared ones (0: H elements)
+  int64_t w_es = 0;         // bytes between experts of wg / wu (0: I rows)
+  int64_t h_ld = 0;         // elements between rows of h (0: I)
   int topk;
   int E;
   int64_t H;
@@ -46,6 +49,9 @@ struct Stage2Params {
   const int32_t* sorted_ids;  // fused only
   const char* wd_shared;    // down weights of expert e_shared ([H, I]) when e_shared >= 0
   int e_shared = -1;        // always-on shared expert's index, or -1
+  int64_t a_ld = 0;         // bytes between rows of a (0: I elements)
+  int64_t wd_ld = 0;        // bytes between rows of wd / wd_shared (0: I elements)
+  int64_t wd_es = 0;        // bytes between experts of wd (0: H rows)
   int E;
   int64_t H;
   int64_t I;

@@ -36,7 +36,7 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
-def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None, device=None):
+def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None, device=None, strided_ok=False):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
     if t.dtype not in dtypes:
@@ -47,8 +47,20 @@ def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None, device=No
         raise ValueError(f"{name} must be a GPU tensor")
     if device is not None and t.device != device:
         raise ValueError(f"{name} is on {t.device}, expected {device}")
-    if not t.is_contiguous():
+    if strided_ok and t.dim() in (2, 3) and t.numel() > 0:
+        # [.., N, K] with unit element stride, rows ld >= K apart and, for a
+        # stack, experts es >= N * ld apart (views of wider or fused tensors)
+        st, N, K = t.stride(), t.shape[-2], t.shape[-1]
+        if st[-1] != 1 or st[-2] < K or (t.dim() == 3 and t.shape[0] > 1 and st[0] < N * st[-2]):
+            raise ValueError(f"{name}: strides {tuple(st)} overlap rows or split them")
+    elif not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+
+
+def _strides(t) -> tuple[int, int]:
+    """(row stride, expert stride) in elements of an [E, N, K] weight stack."""
+    es = t.stride(0) if t.shape[0] > 1 else t.shape[1] * t.stride(1)
+    return t.stride(1), es
 
 
 def _workspace(dev: torch.device, key, nbytes: int) -> torch.Tensor:
@@ -248,6 +260,9 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
     ``shared_expert`` = (w_gate_s [I, H], w_up_s [I, H], w_down_s [H, I]) fp16
     adds an always-on expert with weight 1 in the same launches (fp16 path);
     the returned routing then has k + 1 columns, the last being (E, 1.0).
+    fp16 weights may be strided views (rows and experts apart, e.g. the two
+    halves of a fused [E, 2I, H] gate/up tensor): w_gate and w_up share their
+    strides, the shared expert's rows use the routed experts' row strides.
     Returns fp16 [T, H] (and (ids, weights) when ``return_routing``)."""
     x = hidden_states
     _need(x, "hidden_states", (torch.float16,), 2)
@@ -269,7 +284,9 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
             raise ValueError("router_logits rows != tokens")
     if w8a8 is None:
         for name, t in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down)):
-            _need(t, name, (torch.float16,), 3, dev)
+            _need(t, name, (torch.float16,), 3, dev, strided_ok=True)
+        if _strides(w_gate) != _strides(w_up):
+            raise ValueError("w_gate and w_up must have the same strides")
         I = w_gate.shape[1]
         if tuple(w_gate.shape) != (E, I, H) or tuple(w_up.shape) != (E, I, H) or \
                 tuple(w_down.shape) != (E, H, I):
@@ -292,10 +309,12 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
         if len(shared_expert) != 3:
             raise ValueError("shared_expert is (w_gate, w_up, w_down)")
         for name, t in zip(("w_gate_shared", "w_up_shared", "w_down_shared"), shared_expert):
-            _need(t, name, (torch.float16,), 2, dev)
+            _need(t, name, (torch.float16,), 2, dev, strided_ok=True)
         sg_, su_, sd_ = shared_expert
         if tuple(sg_.shape) != (I, H) or tuple(su_.shape) != (I, H) or tuple(sd_.shape) != (H, I):
             raise ValueError("shared expert shapes do not match [I,H]/[I,H]/[H,I]")
+        if sg_.stride(0) != w_gate.stride(1) or su_.stride(0) != w_up.stride(1) or sd_.stride(0) != w_down.stride(1):
+            raise ValueError("shared expert rows must use the routed experts' row strides")
     if expert_bias is not None:
         _need(expert_bias, "expert_bias", (torch.float32,), 1, dev)
         if expert_bias.numel() != E:
@@ -318,8 +337,20 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
     ws = _workspace(dev, ("fused", w8a8 is not None), nbytes)
     ids = torch.empty((T, ncol), dtype=torch.int32, device=dev) if return_routing else None
     wts = torch.empty((T, ncol), dtype=torch.float32, device=dev) if return_routing else None
+    strided = w8a8 is None and not (w_gate.is_contiguous() and w_up.is_contiguous() and w_down.is_contiguous())
+    if strided:
+        wstr = (ctypes.c_int64 * 4)(*_strides(w_gate), *_strides(w_down))
+        nbytes = L.moe_fused_ex_workspace_bytes(T, H, I, E, top_k, bm, int(shared_expert is not None),
+                                                int(router_weight is not None))
+        ws = _workspace(dev, ("fused", False), nbytes)
     with torch.cuda.device(dev):
-        if shared_expert is not None:
+        if strided:
+            sh = shared_expert if shared_expert is not None else (None, None, None)
+            rc = L.moe_fused_forward_ex(
+                _ptr(x), _ptr(router_logits), _ptr(router_weight), _ptr(expert_bias), _ptr(w_gate), _ptr(w_up),
+                _ptr(w_down), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), wstr, _ptr(out), T, H, I,
+                E, top_k, bm, _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev), None)
+        elif shared_expert is not None:
             rc = L.moe_fused_forward_shared(
                 _ptr(x), _ptr(router_logits), _ptr(router_weight), _ptr(expert_bias), _ptr(w_gate), _ptr(w_up),
                 _ptr(w_down), _ptr(sg_), _ptr(su_), _ptr(sd_), _ptr(out), T, H, I, E, top_k, bm, _ptr(ws),

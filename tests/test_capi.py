@@ -72,6 +72,14 @@ def test_host_validation_without_gpu():
     rc = L.moe_fused_forward_shared(nul, one, nul, nul, nul, nul, nul, one, nul, one, nul, 4, 128, 128, 64, 2,
                                     0, nul, 0, nul, nul, nul)
     assert rc == -1
+    # weight strides that overlap rows or experts, or break 16-byte alignment
+    H, I = 128, 256
+    for st in ((100, 0, 0, 0), (0, 0, 200, 0), (132, 0, 0, 0), (-8, 0, 0, 0), (0, 128 * 255, 0, 0),
+               (0, 0, 0, 128 * 256 - 8), (0, 4 + I * H, 0, 0)):
+        arr = (ctypes.c_int64 * 4)(*st)
+        rc = L.moe_fused_forward_ex(one, one, nul, nul, one, one, one, nul, nul, nul, arr, one, 4, H, I, 8, 2, 0,
+                                    one, 1 << 30, nul, nul, nul, nul)
+        assert rc == -1 and b"weight strides" in L.moe_last_error_string(), st
 
 
 def test_capacity_and_workspace_sizes():
@@ -85,6 +93,10 @@ def test_capacity_and_workspace_sizes():
     assert L.moe_pick_block_m(32, 256, 8) == 32
     ws = L.moe_fused_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 0)
     assert ws >= 32768 * 7168 * 2 + 65280 * 2048 * 2
+    assert L.moe_fused_ex_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 1, 1) == \
+        L.moe_fused_shared_workspace_bytes(4096, 7168, 2048, 256, 8, 128)
+    assert L.moe_fused_ex_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 0, 0) == \
+        L.moe_fused_workspace_bytes(4096, 7168, 2048, 256, 8, 128, 0)
     # the shared expert is expert E, choice k: the fused layout for (E + 1, k + 1)
     # plus the router's partial sums
     assert L.moe_fused_shared_workspace_bytes(4096, 7168, 2048, 256, 8, 128) == \

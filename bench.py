@@ -150,6 +150,8 @@ def main():
     ap.add_argument("--no-check", action="store_true", help="skip the sampled oracle check")
     ap.add_argument("--w8a8", action="store_true", help="run the int8 path (default for --config w8a8)")
     ap.add_argument("--fp16", action="store_true", help="run the fp16 path even for --config w8a8")
+    ap.add_argument("--fp8", action="store_true",
+                    help="run the 8-bit path with OCP fp8 e4m3 codes (f8 MFMA) instead of int8")
     ap.add_argument("--router-gemm", action="store_true",
                     help="also time the router GEMM + routing (x . w_router^T, seeded w_router) alone and "
                          "the fused step started from hidden states (moe_fused_forward_hidden); fp16 only")
@@ -177,7 +179,8 @@ def main():
     torch.cuda.set_device(dev)
     inp = make_inputs(args.config, dev)
     T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
-    w8 = (args.config == "w8a8" or args.w8a8) and not args.fp16
+    w8 = (args.config == "w8a8" or args.w8a8 or args.fp8) and not args.fp16
+    fmt = "fp8" if args.fp8 else "int8"
     L = lib()
     bm = args.block_m or int(L.moe_pick_block_m(T, E, k))
     nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, int(w8))
@@ -196,13 +199,17 @@ def main():
         # weights are quantised once, outside the timed step (they are static)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        qw = m.quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"])
+        qw = m.quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt=fmt)
         b.record()
         torch.cuda.synchronize()
         quant_ms = a.elapsed_time(b)
         cargs = head + [P(t.data_ptr()) for t in (qw.q_gate, qw.s_gate, qw.q_up, qw.s_up, qw.q_down,
                                                    qw.s_down)] + tail
-        fwd, fwd_ev, name = L.moe_fused_forward_w8a8, L.moe_fused_forward_w8a8_events, "moe_fused_forward_w8a8"
+        if fmt == "fp8":
+            fwd = lambda *a: L.moe_fused_forward_fp8(*a, P(0))
+            fwd_ev, name = L.moe_fused_forward_fp8, "moe_fused_forward_fp8"
+        else:
+            fwd, fwd_ev, name = L.moe_fused_forward_w8a8, L.moe_fused_forward_w8a8_events, "moe_fused_forward_w8a8"
     elif args.weights == "w13":
         w13 = torch.cat([inp["wg"], inp["wu"]], dim=1)  # [E, 2I, H]
         wstr = (ctypes.c_int64 * 4)(H, 2 * I * H, 0, 0)
@@ -268,7 +275,8 @@ def main():
     gbs = op_bytes / (ms * 1e-3) / 1e9
     ideal_ms = max(flops / (peak_c * 1e12), op_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3
     s1_hbm_bound = s1_bytes / (PEAK_HBM_GBS * 1e9) >= s1_flops / (peak_c * 1e12)
-    s1_traffic = recorded_traffic(args.config + ("_w8a8" if w8 and args.config != "w8a8" else ""),
+    s1_traffic = recorded_traffic(args.config + ("_fp8" if fmt == "fp8" and w8 else "")
+                                  + ("_w8a8" if w8 and fmt == "int8" and args.config != "w8a8" else ""),
                                   "moe::stage1")  # stage1_kernel / stage1_narrow_kernel
 
     check_res = None
@@ -285,11 +293,12 @@ def main():
         got = out[r].float().cpu()
         tol = lambda ref: bool(torch.isfinite(got).all()) and bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
         if w8:
-            ref8 = w8a8_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), qw.q_gate.cpu().numpy(),
-                                qw.s_gate.cpu().numpy(), qw.q_up.cpu().numpy(), qw.s_up.cpu().numpy(),
-                                qw.q_down.cpu().numpy(), qw.s_down.cpu().numpy(), k, bias_c).float()
+            codes = lambda t: (t.view(torch.uint8) if fmt == "fp8" else t).cpu().numpy()
+            ref8 = w8a8_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), codes(qw.q_gate),
+                                qw.s_gate.cpu().numpy(), codes(qw.q_up), qw.s_up.cpu().numpy(),
+                                codes(qw.q_down), qw.s_down.cpu().numpy(), k, bias_c, fmt=fmt).float()
             check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
-                         "w8a8_oracle_within_rtol2e-2_atol1e-2": tol(ref8),
+                         f"{fmt}_oracle_within_rtol2e-2_atol1e-2": tol(ref8),
                          "rel_l2_vs_fp16_oracle": round(float((got - ref16).norm() / ref16.norm()), 5)}
         else:
             check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
@@ -393,15 +402,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8" if w8 else "fp16",
+        "dtype": (fmt if w8 else "fp16"),
         "data": "synthetic (seeded: x~N(0,1), weights~N(0,0.02), logits~N(0,1)"
                 + (", bias~N(0,0.5)" if CONFIGS[args.config][5] == "normal" else "")
                 + (", bias=-1.2*ln(rank+1)" if CONFIGS[args.config][5] == "zipf" else "") + ")",
         "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} "
-                               + ("W8A8 int8" if w8 else "fp16"),
+                               + (f"W8A8 {fmt}" if w8 else "fp16"),
                    "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
                    "block_m": bm, "experts_touched": int(touched),
-                   "weight_layout": "int8 dense" if w8 else args.weights},
+                   "weight_layout": f"{fmt} dense" if w8 else args.weights},
         "gb_per_s": round(gbs, 1),
         "frac_mfma_peak": round(tflops / peak_c, 4),
         "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),

@@ -227,6 +227,29 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events);
 
+/* ------------------------------------------------------------------------
+ * FP8 (OCP e4m3) variant of the W8A8 path: the same pipeline and scale layout
+ * with e4m3 codes in place of int8 and fp32 accumulation on the gfx950 f8 MFMA
+ * (v_mfma_f32_32x32x64_f8f6f4).  moe_quantize_rows_fp8: per-row scale =
+ * max|row|/448, code = e4m3(w * (448/max|row|)) rounded to nearest even; all-
+ * zero rows give code 0 and scale 0.  Activations are quantised per token and
+ * the SiLU*up intermediate per (row, 128 columns) the same way, inside the call.
+ * moe_fused_forward_fp8 takes stage_events as moe_fused_forward_events (or
+ * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 1).  Extends the
+ * reference's W8A8 variant (submission_v321_int8_fixed.py:421-506) to the fp8
+ * MFMA of this part; the reference has no fp8 path.
+ * ---------------------------------------------------------------------- */
+int moe_quantize_rows_fp8(const void* w, int64_t R, int64_t K, uint8_t* q, float* scale,
+                          void* stream);
+int moe_fused_forward_fp8(const void* x, const float* logits, const float* bias,
+                          const uint8_t* wq_gate, const float* s_gate,
+                          const uint8_t* wq_up, const float* s_up,
+                          const uint8_t* wq_down, const float* s_down, void* out,
+                          int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                          int64_t block_m, void* workspace, int64_t workspace_bytes,
+                          int32_t* topk_ids_out, float* topk_weights_out, void* stream,
+                          void* const* stage_events);
+
 #ifdef __cplusplus
 }
 #endif

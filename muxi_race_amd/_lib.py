@@ -48,6 +48,9 @@ SIGNATURES = {
     "moe_fused_forward_events": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                         _i64, _i64, _p, _i64, _p, _p, _p, _p]),
     "moe_quantize_rows_w8": (_int, [_p, _i64, _i64, _p, _p, _p]),
+    "moe_quantize_rows_fp8": (_int, [_p, _i64, _i64, _p, _p, _p]),
+    "moe_fused_forward_fp8": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                     _i64, _p, _i64, _p, _p, _p, _p]),
     "moe_fused_forward_w8a8": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
     "moe_fused_forward_w8a8_events": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,

@@ -125,7 +125,7 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p1.E = (int)E;
   p1.H = H;
   p1.I = I;
-  int rc = check_launch(moe::launch_stage1(p1, 128, false, false, blocks, s), "stage1");
+  int rc = check_launch(moe::launch_stage1(p1, 128, moe::kQF16, false, blocks, s), "stage1");
   if (rc) return rc;
 
   moe::Stage2Params p2{};
@@ -141,7 +141,7 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p2.H = H;
   p2.I = I;
   p2.V = V;
-  return check_launch(moe::launch_stage2(p2, 128, false, false, blocks, s), "stage2");
+  return check_launch(moe::launch_stage2(p2, 128, moe::kQF16, false, blocks, s), "stage2");
 }
 
 int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k,
@@ -219,13 +219,14 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
 // The always-on shared expert (wg_s / wu_s / wd_s non-null, fp16 only) runs as
 // expert E: every token takes it as choice k with weight 1, so the pipeline
 // works on E + 1 experts and k + 1 choices and the combine adds it last.
-static int fused_common(bool w8, const void* x, const float* logits, const void* w_router, const float* bias,
+static int fused_common(int qt, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
                         const void* wd, const float* sd, const void* wg_s, const void* wu_s,
                         const void* wd_s, const int64_t* wstr, void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                         int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
                         void* const* ev) {
+  const bool w8 = qt != moe::kQF16;  // 8-bit operands: int8 or fp8
   const bool shared = wg_s || wu_s || wd_s;
   if (shared && (w8 || !wg_s || !wu_s || !wd_s))
     return fail(w8 ? MOE_ERR_UNSUPPORTED : MOE_ERR_INVALID_ARG, w8 ? "the shared expert is supported on the fp16 path" : "null pointer argument");
@@ -277,7 +278,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   mark(1);
   if ((rc = check_launch(moe::launch_align(ids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
   mark(2);
-  if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, (int8_t*)(ws + L.xq), (float*)(ws + L.sx), s), "quantize_x"))) return rc;
+  if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, ws + L.xq, (float*)(ws + L.sx), qt, s), "quantize_x"))) return rc;
   mark(3);
 
   moe::Stage1Params p1{};
@@ -302,7 +303,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p1.E = (int)Ee;
   p1.H = H;
   p1.I = I;
-  if ((rc = check_launch(moe::launch_stage1(p1, (int)block_m, w8, true, rows / block_m, s), "stage1"))) return rc;
+  if ((rc = check_launch(moe::launch_stage1(p1, (int)block_m, qt, true, rows / block_m, s), "stage1"))) return rc;
   mark(4);
 
   moe::Stage2Params p2{};
@@ -325,7 +326,7 @@ static int fused_common(bool w8, const void* x, const float* logits, const void*
   p2.E = (int)Ee;
   p2.H = H;
   p2.I = I;
-  if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, w8, true, rows / block_m, s), "stage2"))) return rc;
+  if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, qt, true, rows / block_m, s), "stage2"))) return rc;
   mark(5);
   rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s), "combine");
   mark(6);
@@ -337,7 +338,7 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias, con
                       int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                       int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                       void* stream) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -354,7 +355,7 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream) {
   if (!w_router && T > 0) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(false, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -374,7 +375,7 @@ int moe_fused_forward_shared(const void* x, const float* logits, const void* w_r
                              void* stream) {
   if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
   if (T > 0 && (!w_gate_shared || !w_up_shared || !w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(false, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
+  return fused_common(moe::kQF16, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
                       w_gate_shared, w_up_shared, w_down_shared, nullptr, out, T, H, I, E, k, block_m, workspace,
                       workspace_bytes, topk_ids_out, topk_weights_out, stream, nullptr);
 }
@@ -396,7 +397,7 @@ int moe_fused_forward_ex(const void* x, const float* logits, const void* w_route
   if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
   const bool any = w_gate_shared || w_up_shared || w_down_shared;
   if (T > 0 && any && !(w_gate_shared && w_up_shared && w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(false, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
+  return fused_common(moe::kQF16, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
                       w_gate_shared, w_up_shared, w_down_shared, weight_strides, out, T, H, I, E, k, block_m,
                       workspace, workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
 }
@@ -407,18 +408,39 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events) {
-  return fused_common(false, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }
 
-int moe_quantize_rows_w8(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
-                         void* stream) {
+static int quantize_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt, void* stream) {
   if (R < 0 || K <= 0 || K % 8) return fail(MOE_ERR_INVALID_ARG, "need R >= 0 and K a positive multiple of 8");
   if (R == 0) return MOE_OK;
   if (!w || !q || !scale) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   if (!aligned16(w) || ((uintptr_t)q & 7)) return fail(MOE_ERR_INVALID_ARG, "w must be 16-byte and q 8-byte aligned");
-  return check_launch(moe::launch_quant_rows(w, R, K, q, scale, (hipStream_t)stream), "quantize_rows");
+  return check_launch(moe::launch_quant_rows(w, R, K, q, scale, qt, (hipStream_t)stream), "quantize_rows");
+}
+
+int moe_quantize_rows_w8(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+                         void* stream) {
+  return quantize_rows(w, R, K, q, scale, moe::kQI8, stream);
+}
+
+int moe_quantize_rows_fp8(const void* w, int64_t R, int64_t K, uint8_t* q, float* scale,
+                          void* stream) {
+  return quantize_rows(w, R, K, q, scale, moe::kQF8, stream);
+}
+
+int moe_fused_forward_fp8(const void* x, const float* logits, const float* bias,
+                          const uint8_t* wq_gate, const float* s_gate, const uint8_t* wq_up,
+                          const float* s_up, const uint8_t* wq_down, const float* s_down,
+                          void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                          int64_t block_m, void* workspace, int64_t workspace_bytes,
+                          int32_t* topk_ids_out, float* topk_weights_out, void* stream,
+                          void* const* stage_events) {
+  return fused_common(moe::kQF8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr,
+                      nullptr, nullptr, nullptr, out, T, H, I, E, k, block_m, workspace, workspace_bytes,
+                      topk_ids_out, topk_weights_out, stream, stage_events);
 }
 
 int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias,
@@ -427,7 +449,7 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                            void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                            int64_t block_m, void* workspace, int64_t workspace_bytes,
                            int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -439,7 +461,7 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int64_t block_m, void* workspace, int64_t workspace_bytes,
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events) {
-  return fused_common(true, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }

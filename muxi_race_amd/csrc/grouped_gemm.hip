@@ -55,10 +55,12 @@ __device__ __forceinline__ void with_live(int live, F&& f) {
 // One ring stage holds the tile's token rows, then its weight rows (Stage 1:
 // gate rows, then up rows), ROWS x 128 bytes in all, filled by one DmaTile;
 // fragment reads address it by stage row.
-template <int BM, int WAVES_M, int S, int NW, bool I8, bool GATHER, bool PAIR>
+template <int BM, int WAVES_M, int S, int NW, int QT, bool GATHER, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
+  constexpr bool I8 = QT != kQF16;  // 8-bit operands (int8 or fp8) with row scales
+  constexpr bool F8 = QT == kQF8;
   using L = Layout<BM, WAVES_M, kBN, NW>;
-  using Acc = typename std::conditional<I8, i32x16, f32x16>::type;
+  using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + 2 * kBN;
   using LD = DmaTile<ROWS, NW>;
   constexpr int STAGE = ROWS * kRowBytes;
@@ -162,19 +164,36 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
             uf[buf][a] = frag(st, ur0 + 32 * a, s);
           }
         };
-        load_frags(0, 0);
+        if constexpr (F8) {
+          // fp8: one MFMA per 64-byte half step, on the fragments of two sub-steps
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int fb = s & 1;
-          if (s < 3) load_frags(fb ^ 1, s + 1);
-          __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+          for (int j = 0; j < 2; ++j) {
+            load_frags(0, 2 * j);
+            load_frags(1, 2 * j + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int a = 0; a < L::NBN; ++a)
+            for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-              ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
-              au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
-            }
+              for (int b = 0; b < NB; ++b) {
+                ag[a][b] = mma8(gf[0][a], gf[1][a], xf[0][b], xf[1][b], ag[a][b]);
+                au[a][b] = mma8(uf[0][a], uf[1][a], xf[0][b], xf[1][b], au[a][b]);
+              }
+          }
+        } else {
+          load_frags(0, 0);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int fb = s & 1;
+            if (s < 3) load_frags(fb ^ 1, s + 1);
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+            for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+              for (int b = 0; b < NB; ++b) {
+                ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
+                au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
+              }
+          }
         }
       }
     }
@@ -205,8 +224,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     }
   } else {
     // Dequantise (acc * s_x[token]) * s_w[e, n], h = silu(g) * u, then quantise
-    // h per (row, this 128-column tile): amax over the tile's columns, which
-    // are spread over the lane pair (l, l^32) and the WAVES_N waves.
+    // h per (row, this 128-column tile) to the operands' 8-bit format: amax
+    // over the tile's columns, which are spread over the lane pair (l, l^32)
+    // and the WAVES_N waves.
     float* red = reinterpret_cast<float*>(smem);  // [WAVES_N][BM]; loop ended with a barrier
     float hv[L::NBM][L::NBN][16];
     const float* sgrow = p.sg + (int64_t)e * p.I;
@@ -243,7 +263,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < L::WAVES_N; ++j) amax = fmaxf(amax, red[j * BM + mrow]);
-      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+      const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
       if (mrow < actual) {
         const int64_t grow = row0 + mrow;
         int8_t* hrow = reinterpret_cast<int8_t*>(p.h) + grow * p.h_ld;
@@ -254,14 +274,11 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
             const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
             uint32_t packed = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int qv = quant_i8(hv[b][a][4 * rg + q], inv);
-              packed |= (uint32_t)(qv & 0xff) << (8 * q);
-            }
+            for (int q = 0; q < 4; ++q) packed |= quant_code<F8>(hv[b][a][4 * rg + q], inv) << (8 * q);
             *reinterpret_cast<uint32_t*>(hrow + n) = packed;
           }
         // scales are stored block-major: [I/128][hs_stride]
-        if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = amax / 127.0f;
+        if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = amax / qmax<F8>();
       }
     }
   }
@@ -395,12 +412,14 @@ __global__ __launch_bounds__(256) void stage1_narrow_kernel(Stage1Params p) {
 }
 
 // STREAM: weight tiles no other item reads are loaded non-temporal.
-template <int BM, int WAVES_M, int BN, int S, int NW, bool I8, bool FUSED, bool PAIR, bool STREAM>
+template <int BM, int WAVES_M, int BN, int S, int NW, int QT, bool FUSED, bool PAIR, bool STREAM>
 __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
+  constexpr bool I8 = QT != kQF16;  // 8-bit operands (int8 or fp8) with row / block scales
+  constexpr bool F8 = QT == kQF8;
   using L = Layout<BM, WAVES_M, BN, NW>;
   constexpr int ROWS = BM + BN;
   using LD = DmaTile<ROWS, NW>;
-  constexpr int SCALES = ROWS * kRowBytes;                // int8: row scales of the step
+  constexpr int SCALES = ROWS * kRowBytes;                // 8-bit: row scales of the step
   constexpr int STAGE = SCALES + (I8 ? 256 * NW : 0);
   static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
@@ -508,28 +527,42 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
               for (int b = 0; b < NB; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
           }
         } else {
-          // One K step of int8 is one 128-column scale block of the
-          // intermediate: exact int32 partial product, then
-          // acc += partial * s_h[row, block].
+          // One K step of 8-bit operands is one 128-column scale block of the
+          // intermediate: partial product (exact int32 for int8, fp32 for
+          // fp8), then acc += partial * s_h[row, block].
           const float* scl = reinterpret_cast<const float*>(st + SCALES);
           float sc[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) sc[b] = scl[xr0 + 32 * b + (l & 31)];
-          i32x16 ia[L::NBN][NB];
+          using PAcc = typename std::conditional<F8, f32x16, i32x16>::type;
+          PAcc ia[L::NBN][NB];
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) ia[a][b] = i32x16{};
-          load_frags(0, 0);
+            for (int b = 0; b < NB; ++b) ia[a][b] = PAcc{};
+          if constexpr (F8) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int fb = s & 1;
-            if (s < 3) load_frags(fb ^ 1, s + 1);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int j = 0; j < 2; ++j) {
+              load_frags(0, 2 * j);
+              load_frags(1, 2 * j + 1);
+              __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int a = 0; a < L::NBN; ++a)
+              for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-              for (int b = 0; b < NB; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
+                for (int b = 0; b < NB; ++b) ia[a][b] = mma8(wf[0][a], wf[1][a], af[0][b], af[1][b], ia[a][b]);
+            }
+          } else {
+            load_frags(0, 0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int fb = s & 1;
+              if (s < 3) load_frags(fb ^ 1, s + 1);
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
+            }
           }
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a)
@@ -642,10 +675,10 @@ constexpr int s2_stages(int bm) {
 #define MOE_S1N_STAGES 6
 #endif
 
-template <int BM, int WM, int NW, bool I8, bool GATHER, bool PAIR>
+template <int BM, int WM, int NW, int QT, bool GATHER, bool PAIR>
 static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
   constexpr int kS = s1_stages(BM);
-  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, NW, I8, GATHER, PAIR>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((stage1_kernel<BM, WM, kS, NW, QT, GATHER, PAIR>), dim3((unsigned)grid),
                      dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
@@ -654,27 +687,27 @@ static hipError_t go1(const Stage1Params& p, int64_t grid, hipStream_t s) {
 // 256-wide N tile when H allows: half the workgroups, half the re-reads of the
 // intermediate, and twice the work behind each workgroup's pipeline fill and
 // epilogue.  Paired items are then 256 x 128.
-template <int BM, int WM, int BN, int NW, bool I8, bool FUSED, bool PAIR>
+template <int BM, int WM, int BN, int NW, int QT, bool FUSED, bool PAIR>
 static hipError_t go2(const Stage2Params& p, int64_t max_blocks, hipStream_t s) {
   constexpr int kS = s2_stages(BM);
   const int64_t grid = schedule_grid(max_blocks, p.H / BN);
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, I8, FUSED, PAIR, BM == 32>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((stage2_kernel<BM, WM, BN, kS, NW, QT, FUSED, PAIR, BM == 32>), dim3((unsigned)grid),
                      dim3(64 * NW), 0, s, p);
   return hipGetLastError();
 }
-template <bool I8, bool FUSED>
+template <int QT, bool FUSED>
 static hipError_t go2_128(const Stage2Params& p, int64_t mb, hipStream_t s) {
   constexpr int NW = MOE_S2_WAVES_128;
-  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, NW, I8, FUSED, MOE_PAIR != 0>(p, mb, s);
-  return go2<128, 2, 128, NW, I8, FUSED, false>(p, mb, s);
+  if (MOE_S2_BN_128 == 256 && p.H % 256 == 0) return go2<128, 2, 256, NW, QT, FUSED, MOE_PAIR != 0>(p, mb, s);
+  return go2<128, 2, 128, NW, QT, FUSED, false>(p, mb, s);
 }
 
-hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, bool gather,
+hipError_t launch_stage1(const Stage1Params& params, int block_m, int qt, bool gather,
                          int64_t max_blocks, hipStream_t s) {
   Stage1Params p = params;
   p.host_blocks = (int)max_blocks;
-  if (p.w_ld == 0) p.w_ld = p.H * (int8 ? 1 : 2);
+  if (p.w_ld == 0) p.w_ld = p.H * (qt != kQF16 ? 1 : 2);
   if (p.w_es == 0) p.w_es = p.I * p.w_ld;
   if (p.h_ld == 0) p.h_ld = p.I;
   const int64_t grid = schedule_grid(max_blocks, p.I / kBN);
@@ -682,45 +715,57 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, bool int8, boo
   constexpr int NW = MOE_S1_WAVES_128;
   constexpr bool kPair = MOE_PAIR != 0;
   if (!gather) {
-    if (block_m == 128 && !int8) return go1<128, 2, NW, false, false, kPair>(p, grid, s);
+    if (block_m == 128 && qt == kQF16) return go1<128, 2, NW, kQF16, false, kPair>(p, grid, s);
     return hipErrorInvalidValue;
   }
   switch (block_m) {
     case 32:
-      if (int8) return go1<32, 1, 4, true, true, false>(p, grid, s);
+      if (qt == kQI8) return go1<32, 1, 4, kQI8, true, false>(p, grid, s);
+      if (qt == kQF8) return go1<32, 1, 4, kQF8, true, false>(p, grid, s);
       if constexpr (MOE_S1_NARROW32 != 0) {
         constexpr int kW = MOE_S1_NARROW32;
         const int64_t gn = schedule_grid(max_blocks, p.I / kW);
         hipLaunchKernelGGL((stage1_narrow_kernel<kW, MOE_S1N_STAGES>), dim3((unsigned)gn), dim3(256), 0, s, p);
         return hipGetLastError();
       }
-      return go1<32, 1, 4, false, true, false>(p, grid, s);
+      return go1<32, 1, 4, kQF16, true, false>(p, grid, s);
     case 64:
-      return int8 ? go1<64, 1, 4, true, true, false>(p, grid, s) : go1<64, 1, 4, false, true, false>(p, grid, s);
+      if (qt == kQI8) return go1<64, 1, 4, kQI8, true, false>(p, grid, s);
+      if (qt == kQF8) return go1<64, 1, 4, kQF8, true, false>(p, grid, s);
+      return go1<64, 1, 4, kQF16, true, false>(p, grid, s);
     case 128:
-      return int8 ? go1<128, 2, NW, true, true, false>(p, grid, s) : go1<128, 2, NW, false, true, kPair>(p, grid, s);
+      if (qt == kQI8) return go1<128, 2, NW, kQI8, true, false>(p, grid, s);
+      if (qt == kQF8) return go1<128, 2, NW, kQF8, true, false>(p, grid, s);
+      return go1<128, 2, NW, kQF16, true, kPair>(p, grid, s);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_stage2(const Stage2Params& params, int block_m, bool int8, bool fused,
+hipError_t launch_stage2(const Stage2Params& params, int block_m, int qt, bool fused,
                          int64_t max_blocks, hipStream_t s) {
   Stage2Params p = params;
   p.host_blocks = (int)max_blocks;
-  if (p.a_ld == 0) p.a_ld = p.I * (int8 ? 1 : 2);
-  if (p.wd_ld == 0) p.wd_ld = p.I * (int8 ? 1 : 2);
+  if (p.a_ld == 0) p.a_ld = p.I * (qt != kQF16 ? 1 : 2);
+  if (p.wd_ld == 0) p.wd_ld = p.I * (qt != kQF16 ? 1 : 2);
   if (p.wd_es == 0) p.wd_es = p.H * p.wd_ld;
   const int64_t mb = max_blocks;
   if (!fused) {
-    if (block_m == 128 && !int8) return go2_128<false, false>(p, mb, s);
+    if (block_m == 128 && qt == kQF16) return go2_128<kQF16, false>(p, mb, s);
     return hipErrorInvalidValue;
   }
   switch (block_m) {
     case 32:
-      return int8 ? go2<32, 1, kBN, 4, true, true, false>(p, mb, s) : go2<32, 1, kBN, 4, false, true, false>(p, mb, s);
+      if (qt == kQI8) return go2<32, 1, kBN, 4, kQI8, true, false>(p, mb, s);
+      if (qt == kQF8) return go2<32, 1, kBN, 4, kQF8, true, false>(p, mb, s);
+      return go2<32, 1, kBN, 4, kQF16, true, false>(p, mb, s);
     case 64:
-      return int8 ? go2<64, 1, kBN, 4, true, true, false>(p, mb, s) : go2<64, 1, kBN, 4, false, true, false>(p, mb, s);
-    case 128: return int8 ? go2_128<true, true>(p, mb, s) : go2_128<false, true>(p, mb, s);
+      if (qt == kQI8) return go2<64, 1, kBN, 4, kQI8, true, false>(p, mb, s);
+      if (qt == kQF8) return go2<64, 1, kBN, 4, kQF8, true, false>(p, mb, s);
+      return go2<64, 1, kBN, 4, kQF16, true, false>(p, mb, s);
+    case 128:
+      if (qt == kQI8) return go2_128<kQI8, true>(p, mb, s);
+      if (qt == kQF8) return go2_128<kQF8, true>(p, mb, s);
+      return go2_128<kQF16, true>(p, mb, s);
   }
   return hipErrorInvalidValue;
 }

@@ -6,6 +6,11 @@
 
 namespace moe {
 
+// Operand formats of the expert GEMMs: fp16, or 8-bit codes with fp32 row
+// scales -- int8 (i8 MFMA, int32 accumulation) or OCP fp8 e4m3 (f8 MFMA, fp32
+// accumulation).
+enum QuantType : int { kQF16 = 0, kQI8 = 1, kQF8 = 2 };
+
 // Stage 1: h = silu(X Wg^T) * (X Wu^T) for the rows of every M block.
 struct Stage1Params {
   const char* x;            // fp16 [rows, H] (direct) / fp16|int8 [T, H] (gather)
@@ -59,9 +64,10 @@ struct Stage2Params {
   int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher)
 };
 
-hipError_t launch_stage1(const Stage1Params& p, int block_m, bool int8, bool gather,
+// qt: a QuantType
+hipError_t launch_stage1(const Stage1Params& p, int block_m, int qt, bool gather,
                          int64_t max_blocks, hipStream_t stream);
-hipError_t launch_stage2(const Stage2Params& p, int block_m, bool int8, bool fused,
+hipError_t launch_stage2(const Stage2Params& p, int block_m, int qt, bool fused,
                          int64_t max_blocks, hipStream_t stream);
 
 // With e_shared >= 0 every token also gets the shared expert as choice k
@@ -95,7 +101,9 @@ hipError_t launch_router(const void* x, const void* w_router, const float* bias,
                          int e_shared = -1);
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream);
-hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+// Per-row 8-bit quantisation of an fp16 [R, K] matrix to the format qt
+// (kQI8 or kQF8): codes into q, amax / qmax into scale.
+hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,
                              hipStream_t stream);
 
 }  // namespace moe

@@ -27,6 +27,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -178,6 +179,17 @@ __device__ __forceinline__ i32x16 mma(u32x4 a, u32x4 b, i32x16 c) {
                                               __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
+// fp8 (OCP e4m3) x fp8 over 64 K elements: the lane supplies 32 bytes, the
+// fragments of two consecutive 32-byte K sub-steps (frag(.., s) and
+// frag(.., s + 1)).  Which K index each byte takes does not matter as long as
+// both operands come from the same LDS layout through the same fragment loads.
+__device__ __forceinline__ f32x16 mma8(u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1, f32x16 c) {
+  const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+  const i32x8 b = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+  // format 0 (fp8 e4m3) for both operands, no block scaling
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // silu(g) * u = u * g / (1 + 2^(-g*log2e)) in fp32 (v_exp_f32 + v_rcp_f32).
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));
@@ -195,6 +207,39 @@ __device__ __forceinline__ int quant_i8(float x, float inv) {
   q = q > 127 ? 127 : q;
   q = q < -127 ? -127 : q;
   return q;
+}
+
+// OCP fp8 e4m3 code of v, round to nearest even, saturating at +-448 (the
+// callers scale so that |v| <= 448).  Normals: the fp32 mantissa is rounded to
+// 3 bits with the carry running into the exponent, which is rebiased 127 -> 7;
+// below 2^-6 the code is the multiple of 2^-9 (rint is round-to-even).
+__device__ __forceinline__ uint32_t f8_e4m3(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = __builtin_fabsf(v);
+  uint32_t code;
+  if (a >= 0.015625f) {
+    const uint32_t au = __float_as_uint(a);
+    code = ((au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20) - (120u << 3);
+    code = code > 0x7Eu ? 0x7Eu : code;
+  } else {
+    code = (uint32_t)__builtin_rintf(a * 512.0f);
+  }
+  return sign | code;
+}
+
+// Largest code magnitude of the 8-bit formats: int8 (symmetric) and fp8 e4m3.
+template <bool F8> constexpr float qmax() { return F8 ? 448.0f : 127.0f; }
+
+// 8-bit code (low byte) of x * inv: int8 round-half-away or fp8 e4m3.
+template <bool F8>
+__device__ __forceinline__ uint32_t quant_code(float x, float inv) {
+  if constexpr (F8) {
+#pragma clang fp contract(off)
+    return f8_e4m3(x * inv);
+  } else {
+    return (uint32_t)quant_i8(x, inv) & 0xffu;
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -366,25 +366,23 @@ hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void*
 // of up to 64 * 8 * NCH elements are held in registers (all NCH chunk loads
 // in flight at once, one pass over memory); longer rows take two passes.
 // ---------------------------------------------------------------------------
+template <bool F8>
 __device__ __forceinline__ u32x2 quant_pack8(f16x8 v, float inv) {
   u32x2 packed = {0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int qv = quant_i8((float)v[i], inv);
-    packed[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
-  }
+  for (int i = 0; i < 8; ++i) packed[i >> 2] |= quant_code<F8>((float)v[i], inv) << (8 * (i & 3));
   return packed;
 }
 
-template <int NCH>
+template <int NCH, bool F8>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ w, int64_t R,
-                                                         int64_t K, int8_t* __restrict__ q,
+                                                         int64_t K, uint8_t* __restrict__ q,
                                                          float* __restrict__ scale) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int l = lane_id();
   if (r >= R) return;
   const _Float16* row = w + r * K;
-  int8_t* qrow = q + r * K;
+  uint8_t* qrow = q + r * K;
   float amax = 0.0f;
   if constexpr (NCH > 0) {
     f16x8 v[NCH];
@@ -398,11 +396,11 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[j][i]));
     amax = wave_max(amax);
-    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int64_t c = 512 * j + 8 * l;
-      if (c < K) *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8(v[j], inv);
+      if (c < K) *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(v[j], inv);
     }
   } else {
     for (int64_t c = 8 * l; c < K; c += 512) {
@@ -411,23 +409,32 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
     }
     amax = wave_max(amax);
-    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
     for (int64_t c = 8 * l; c < K; c += 512)
-      *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8(*reinterpret_cast<const f16x8*>(row + c), inv);
+      *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(*reinterpret_cast<const f16x8*>(row + c), inv);
   }
-  if (l == 0) scale[r] = amax / 127.0f;
+  if (l == 0) scale[r] = amax / qmax<F8>();
 }
 
-hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
+hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,
                              hipStream_t s) {
   if (R == 0) return hipSuccess;
   const dim3 grid((unsigned)((R + 3) / 4)), block(256);
   const _Float16* src = reinterpret_cast<const _Float16*>(w);
+  uint8_t* dst = reinterpret_cast<uint8_t*>(q);
   const int64_t nch = (K + 511) / 512;
-  if (nch <= 4) hipLaunchKernelGGL(quant_rows_kernel<4>, grid, block, 0, s, src, R, K, q, scale);
-  else if (nch <= 8) hipLaunchKernelGGL(quant_rows_kernel<8>, grid, block, 0, s, src, R, K, q, scale);
-  else if (nch <= 16) hipLaunchKernelGGL(quant_rows_kernel<16>, grid, block, 0, s, src, R, K, q, scale);
-  else hipLaunchKernelGGL(quant_rows_kernel<0>, grid, block, 0, s, src, R, K, q, scale);
+#define MOE_QR(N)                                                                               \
+  do {                                                                                          \
+    if (qt == kQF8)                                                                             \
+      hipLaunchKernelGGL((quant_rows_kernel<N, true>), grid, block, 0, s, src, R, K, dst, scale);  \
+    else                                                                                        \
+      hipLaunchKernelGGL((quant_rows_kernel<N, false>), grid, block, 0, s, src, R, K, dst, scale); \
+  } while (0)
+  if (nch <= 4) MOE_QR(4);
+  else if (nch <= 8) MOE_QR(8);
+  else if (nch <= 16) MOE_QR(16);
+  else MOE_QR(0);
+#undef MOE_QR
   return hipGetLastError();
 }
 

@@ -213,35 +213,45 @@ def fused_workspace_bytes(T, H, I, E, top_k, block_m=0, w8a8=False) -> int:
 # ---------------------------------------------------------------------------
 # W8A8
 # ---------------------------------------------------------------------------
-def quantize_rows_w8(w: torch.Tensor):
-    """Per-row int8 of an fp16 tensor [..., K]: (q int8 [..., K], scale fp32 [...])."""
+def quantize_rows_w8(w: torch.Tensor, fmt: str = "int8"):
+    """Per-row 8-bit quantisation of an fp16 tensor [..., K]: (q [..., K],
+    scale fp32 [...]).  fmt "int8": q int8, scale = max|row|/127; "fp8": q
+    torch.float8_e4m3fn (OCP e4m3, round to nearest even), scale = max|row|/448."""
     _need(w, "w", (torch.float16,))
+    if fmt not in ("int8", "fp8"):
+        raise ValueError(f"fmt must be 'int8' or 'fp8', got {fmt!r}")
     dev = w.device
     K = w.shape[-1]
     R = w.numel() // K if K else 0
-    q = torch.empty(w.shape, dtype=torch.int8, device=dev)
+    q = torch.empty(w.shape, dtype=torch.int8 if fmt == "int8" else torch.float8_e4m3fn, device=dev)
     s = torch.empty(w.shape[:-1], dtype=torch.float32, device=dev)
+    fn = lib().moe_quantize_rows_w8 if fmt == "int8" else lib().moe_quantize_rows_fp8
     with torch.cuda.device(dev):
-        rc = lib().moe_quantize_rows_w8(_ptr(w), R, K, _ptr(q), _ptr(s), _stream(dev))
-    check(rc, "quantize_rows_w8")
+        rc = fn(_ptr(w), R, K, _ptr(q), _ptr(s), _stream(dev))
+    check(rc, "quantize_rows_" + fmt)
     return q, s
 
 
 @dataclass
 class W8A8Weights:
-    """Per-output-row int8 expert weights with fp32 scales."""
-    q_gate: torch.Tensor   # int8 [E, I, H]
+    """Per-output-row 8-bit expert weights with fp32 scales: int8 codes, or
+    fp8 e4m3 codes (torch.float8_e4m3fn) for the fp8 variant."""
+    q_gate: torch.Tensor   # int8 | float8_e4m3fn [E, I, H]
     s_gate: torch.Tensor   # fp32 [E, I]
     q_up: torch.Tensor
     s_up: torch.Tensor
-    q_down: torch.Tensor   # int8 [E, H, I]
+    q_down: torch.Tensor   # int8 | float8_e4m3fn [E, H, I]
     s_down: torch.Tensor   # fp32 [E, H]
 
+    @property
+    def fmt(self) -> str:
+        return "fp8" if self.q_gate.dtype == torch.float8_e4m3fn else "int8"
 
-def quantize_w8a8_weights(w_gate, w_up, w_down) -> W8A8Weights:
-    qg, sg = quantize_rows_w8(w_gate)
-    qu, su = quantize_rows_w8(w_up)
-    qd, sd = quantize_rows_w8(w_down)
+
+def quantize_w8a8_weights(w_gate, w_up, w_down, fmt: str = "int8") -> W8A8Weights:
+    qg, sg = quantize_rows_w8(w_gate, fmt)
+    qu, su = quantize_rows_w8(w_up, fmt)
+    qd, sd = quantize_rows_w8(w_down, fmt)
     return W8A8Weights(qg, sg, qu, su, qd, sd)
 
 
@@ -254,7 +264,8 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
     """Full MoE FFN: softmax/top-k/renormalise routing, expert SwiGLU MLPs,
     routing-weighted combine.  hidden_states fp16 [T, H], router_logits fp32
     [T, E], w_gate/w_up fp16 [E, I, H], w_down fp16 [E, H, I] (or ``w8a8``
-    quantised weights, in which case w_gate/w_up/w_down may be None).
+    quantised weights, int8 or fp8, in which case w_gate/w_up/w_down may be
+    None).
     With ``router_weight`` (fp16 [E, H]) and router_logits None (fp16 path
     only), the logits are computed in the same call by the router GEMM.
     ``shared_expert`` = (w_gate_s [I, H], w_up_s [I, H], w_down_s [H, I]) fp16
@@ -293,9 +304,12 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
             raise ValueError("expert weight shapes do not match [E,I,H]/[E,I,H]/[E,H,I]")
     else:
         q = w8a8
-        _need(q.q_gate, "q_gate", (torch.int8,), 3, dev)
-        _need(q.q_up, "q_up", (torch.int8,), 3, dev)
-        _need(q.q_down, "q_down", (torch.int8,), 3, dev)
+        qdt = q.q_gate.dtype
+        if qdt not in (torch.int8, torch.float8_e4m3fn):
+            raise TypeError(f"q_gate: dtype {qdt} is neither int8 nor float8_e4m3fn")
+        _need(q.q_gate, "q_gate", (qdt,), 3, dev)
+        _need(q.q_up, "q_up", (qdt,), 3, dev)
+        _need(q.q_down, "q_down", (qdt,), 3, dev)
         for name, t in (("s_gate", q.s_gate), ("s_up", q.s_up), ("s_down", q.s_down)):
             _need(t, name, (torch.float32,), 2, dev)
         I = q.q_gate.shape[1]
@@ -363,6 +377,12 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
             rc = L.moe_fused_forward(_ptr(x), _ptr(router_logits), _ptr(expert_bias), _ptr(w_gate),
                                      _ptr(w_up), _ptr(w_down), _ptr(out), T, H, I, E, top_k, bm,
                                      _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev))
+        elif w8a8.fmt == "fp8":
+            q = w8a8
+            rc = L.moe_fused_forward_fp8(
+                _ptr(x), _ptr(router_logits), _ptr(expert_bias), _ptr(q.q_gate), _ptr(q.s_gate),
+                _ptr(q.q_up), _ptr(q.s_up), _ptr(q.q_down), _ptr(q.s_down), _ptr(out), T, H, I, E,
+                top_k, bm, _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev), None)
         else:
             q = w8a8
             rc = L.moe_fused_forward_w8a8(

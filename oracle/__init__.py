@@ -28,6 +28,14 @@ Pinning (how each function is checked independently of its own formula):
                            hand-made rows, round-half-away edge cases, and the
                            fp16 oracle within the north-star W8A8 gate
                            (tests/test_oracle_w8a8.py).
+* ``fp8_e4m3_codes`` / ``quantize_rows_fp8`` / ``w8a8_forward(fmt="fp8")`` --
+                           torch's own float8_e4m3fn conversion on every code
+                           boundary and midpoint (ties to even), hand-made
+                           codes, the e4m3 value table against the format's
+                           definition, and the fp16 oracle within the W8A8
+                           gate (tests/test_oracle_fp8.py).
+* ``fused_moe_forward(shared=)`` -- exact doubling closed form and the dense
+                           SwiGLU difference (tests/test_oracle_core.py).
 """
 
 from .moe_ref import (  # noqa: F401
@@ -40,6 +48,9 @@ from .moe_ref import (  # noqa: F401
     combine,
     fused_moe_forward,
     quantize_rows_int8,
+    quantize_rows_fp8,
+    fp8_e4m3_codes,
+    FP8_E4M3_VALUES,
     w8a8_forward,
     silu_mul,
 )

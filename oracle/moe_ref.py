@@ -259,29 +259,87 @@ def quantize_rows_int8(w):
     return q, scale
 
 
+def fp8_e4m3_codes(v) -> np.ndarray:
+    """OCP fp8 e4m3 codes (uint8) of float32 values, round to nearest even,
+    saturating at +-448: normals round the fp32 mantissa to 3 bits (carry into
+    the exponent) and rebias the exponent 127 -> 7; below 2**-6 the code is
+    the nearest-even multiple of 2**-9."""
+    v = np.asarray(v, dtype=np.float32)
+    u = v.view(np.uint32)
+    sign = ((u >> 24) & 0x80).astype(np.uint32)
+    a = np.abs(v)
+    au = a.view(np.uint32).astype(np.uint64)
+    normal = ((au + 0x7FFFF + ((au >> 20) & 1)) >> 20).astype(np.int64) - (120 << 3)
+    normal = np.minimum(normal, 0x7E)
+    sub = np.rint((a * np.float32(512.0)).astype(np.float32)).astype(np.int64)
+    code = np.where(a >= np.float32(0.015625), normal, sub)
+    return (sign | code.astype(np.uint32)).astype(np.uint8)
+
+
+def _fp8_table() -> np.ndarray:
+    """float64 value of each of the 256 e4m3 codes (0x7F / 0xFF are NaN)."""
+    c = np.arange(256)
+    e, m = (c >> 3) & 0xF, c & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7.0))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return np.where(c & 0x80, -mag, mag)
+
+
+FP8_E4M3_VALUES = _fp8_table()
+
+
+def quantize_rows_fp8(w):
+    """Per-row fp8 e4m3: amax = max|w|, scale = amax/448, code =
+    e4m3(w * (448/amax)) (product rounded to fp32, then to e4m3 nearest even).
+    Rows with amax == 0 give code 0 and scale 0.  Returns (codes uint8
+    [..., K], scale float32 [...])."""
+    a = _as_t(w).float().numpy().astype(np.float32)
+    amax = np.abs(a).max(axis=-1).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(amax > 0, np.float32(448.0) / amax, np.float32(0.0)).astype(np.float32)
+    scale = (amax / np.float32(448.0)).astype(np.float32)
+    return fp8_e4m3_codes((a * inv[..., None]).astype(np.float32)), scale
+
+
 def _int_matmul(a: np.ndarray, b_t: np.ndarray) -> np.ndarray:
     """Exact int8 x int8 -> integer product a @ b_t.T (float64 BLAS is exact
     here: |sum| <= 127*127*K < 2**53)."""
     return np.rint(a.astype(np.float64) @ b_t.astype(np.float64).T).astype(np.int64)
 
 
-def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k: int,
-                 bias=None, block_m: int = 128, *, scale_block: int = 128, experts=None):
-    """W8A8 fused MoE on the CPU (the GPU path's exact arithmetic contract).
+def _exact_matmul(a: np.ndarray, b_t: np.ndarray) -> np.ndarray:
+    """a @ b_t.T in float64 for 8-bit operand values (int8 or e4m3): exact,
+    as the integer or 2**-18-grid sums stay below 2**53 ulps."""
+    return a.astype(np.float64) @ b_t.astype(np.float64).T
 
-    x rows are quantised per token; gate/up are exact int GEMMs dequantised as
-    (acc * s_x[t]) * s_w[e, n]; h = silu(g) * u is quantised per (row,
+
+def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k: int,
+                 bias=None, block_m: int = 128, *, scale_block: int = 128, experts=None, fmt="int8"):
+    """W8A8 fused MoE on the CPU (the GPU path's arithmetic contract).
+
+    x rows are quantised per token; gate/up are exact 8-bit GEMMs dequantised
+    as (acc * s_x[t]) * s_w[e, n]; h = silu(g) * u is quantised per (row,
     ``scale_block`` columns); the down GEMM accumulates each column block's
-    exact int product times its row scale, in block order, then applies
+    exact product times its row scale, in block order, then applies
     s_down[e, n] and the routing weight; pairs are combined in choice order.
+    fmt "int8": int8 codes (wq_* int8); "fp8": OCP e4m3 codes (wq_* uint8),
+    whose products are exact in float64 (8 significant bits each, sums of at
+    most 2**14 terms between 2**-18 and 2**18); the GPU sums them in fp32.
     """
+    if fmt == "fp8":
+        quant = quantize_rows_fp8
+        val = lambda c: FP8_E4M3_VALUES[np.asarray(c, dtype=np.uint8)]
+    else:
+        quant = quantize_rows_int8
+        val = lambda c: np.asarray(c)
     x = _as_t(x)
     T, H = x.shape
     E, I, _ = wq_gate.shape
     ids, w = route_topk(_as_t(logits).float().numpy(), top_k,
                         None if bias is None else _as_t(bias).float().numpy())
     al = align(ids, E, block_m)
-    xq, sx = quantize_rows_int8(x)
+    xq, sx = quant(x)
+    xq = val(xq)
     P = T * top_k
     gs, go = al["group_sizes"], al["group_offsets"]
     order = al["sorted_pair_ids"]
@@ -294,17 +352,19 @@ def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k
         pairs = order[al["group_padded_offsets"][e] : al["group_padded_offsets"][e] + n].astype(np.int64)
         tok = pairs // top_k
         a = xq[tok]
-        g = (_int_matmul(a, wq_gate[e]).astype(np.float32) * sx[tok][:, None]).astype(np.float32)
+        g = (_exact_matmul(a, val(wq_gate[e])).astype(np.float32) * sx[tok][:, None]).astype(np.float32)
         g = (g * s_gate[e][None, :]).astype(np.float32)
-        u = (_int_matmul(a, wq_up[e]).astype(np.float32) * sx[tok][:, None]).astype(np.float32)
+        u = (_exact_matmul(a, val(wq_up[e])).astype(np.float32) * sx[tok][:, None]).astype(np.float32)
         u = (u * s_up[e][None, :]).astype(np.float32)
         h = silu_mul(torch.from_numpy(g), torch.from_numpy(u)).numpy().astype(np.float32)
         nb = I // scale_block
         hb = h.reshape(n, nb, scale_block)
-        hq, sh = quantize_rows_int8(hb)          # [n, nb, 128], [n, nb]
+        hq, sh = quant(hb)                       # [n, nb, 128], [n, nb]
+        hq = val(hq)
+        wd = val(wq_down[e])
         acc = np.zeros((n, H), dtype=np.float32)
         for b in range(nb):
-            part = _int_matmul(hq[:, b, :], wq_down[e][:, b * scale_block:(b + 1) * scale_block])
+            part = _exact_matmul(hq[:, b, :], wd[:, b * scale_block:(b + 1) * scale_block])
             acc = (acc + part.astype(np.float32) * sh[:, b : b + 1]).astype(np.float32)
         y = (acc * s_down[e][None, :]).astype(np.float32)
         y = (y * wflat[pairs][:, None]).astype(np.float32)

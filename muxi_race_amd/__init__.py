@@ -20,4 +20,6 @@ from .moe import (  # noqa: F401
     run_kernel,
 )
 
+from .weights import load_w8a8, save_w8a8  # noqa: F401,E402
+
 __version__ = "0.1.0"

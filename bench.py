@@ -85,6 +85,18 @@ class HipEvents:
             self.hip.hipEventDestroy(ctypes.c_void_p(e))
 
 
+def cpu_model() -> str:
+    """The host CPU's model string (lscpu's "Model name") from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(inp, ids_np, budget_s=15.0):
     """The oracle's fp32 expert loop (problem_detail.json:50 restated) on a
     bounded sample of experts of this routing, timed on the host; returns
@@ -119,8 +131,8 @@ def cpu_baseline(inp, ids_np, budget_s=15.0):
                 kind="port",
                 sample=(f"oracle fp32 per-expert loop (torch CPU) over {len(used)} of {len(order)} "
                         f"routed experts = {done_rows} of {T * k} routed rows, {spent:.1f} s; "
-                        f"routing/align/combine excluded; host {platform.processor() or 'x86_64'}, "
-                        f"os.cpu_count()={os.cpu_count()}"))
+                        f"routing/align/combine excluded; host {cpu_model()}, "
+                        f"os.cpu_count()={os.cpu_count()}, torch threads={torch.get_num_threads()}"))
 
 
 def recorded_traffic(config, kernel_prefix):
@@ -143,7 +155,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=30)  # ~0.17 s at dsv3: clocks settle before timing
     ap.add_argument("--config", default="dsv3", choices=list(CONFIGS))
     ap.add_argument("--block-m", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -185,7 +197,7 @@ def main():
     bm = args.block_m or int(L.moe_pick_block_m(T, E, k))
     nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, int(w8))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    out = torch.full((T, H), float("nan"), dtype=torch.float16, device=dev)  # poisoned: the step must write it all
     ids = torch.empty((T, k), dtype=torch.int32, device=dev)
     wts = torch.empty((T, k), dtype=torch.float32, device=dev)
     P = ctypes.c_void_p
@@ -303,6 +315,7 @@ def main():
         else:
             check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
                          "within_rtol2e-2_atol1e-2": tol(ref16)}
+        check_res["output_all_finite"] = bool(torch.isfinite(out).all())  # out was NaN-poisoned
 
     cpu = None if args.no_cpu else cpu_baseline(inp, ids_np)
 

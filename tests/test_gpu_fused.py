@@ -55,6 +55,11 @@ def test_mixtral_sampled():
     _check(moe_inputs("mixtral", 4), sample=24, what="mixtral")
 
 
+def test_mixtral_ragged():
+    # H = 4096 takes Stage 2's 256-wide N tiles; T = 700 leaves ragged last blocks
+    _check(moe_inputs("mixtral", 9, T=700), sample=40, block_m=128, what="mixtral T=700")
+
+
 def test_dsv3_sampled():
     _check(moe_inputs("dsv3", 5), sample=8, what="dsv3")
 

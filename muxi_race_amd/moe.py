@@ -64,7 +64,11 @@ def _strides(t) -> tuple[int, int]:
 
 
 def _workspace(dev: torch.device, key, nbytes: int) -> torch.Tensor:
-    k = (dev.index, key)
+    """Scratch reused across calls, one per (device, stream, use): calls on
+    different streams never share one (they may run concurrently), and a
+    buffer is allocated on the stream that uses it, so replacing it by a
+    larger one is ordered after that stream's earlier kernels."""
+    k = (dev.index, torch.cuda.current_stream(dev).cuda_stream, key)
     buf = _WORKSPACE.get(k)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)

@@ -78,3 +78,26 @@ def test_repeat_is_bitwise_deterministic():
     for _ in range(3):
         b, _, _ = _gpu(inp)
         assert torch.equal(a, b)
+
+
+def test_two_streams_do_not_share_scratch():
+    """Calls on two streams (default priority) may overlap: each gets its own
+    workspace, so both results equal the one-stream results."""
+    from muxi_race_amd import fused_moe
+    a_in, b_in = moe_inputs("small", 10, T=384), moe_inputs("decode", 11)
+    ra, _, _ = _gpu(a_in)
+    rb, _, _ = _gpu(b_in)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            oa = fused_moe(a_in["x"], a_in["logits"], a_in["wg"], a_in["wu"], a_in["wd"], a_in["k"],
+                           expert_bias=a_in["bias"])
+        with torch.cuda.stream(s2):
+            ob = fused_moe(b_in["x"], b_in["logits"], b_in["wg"], b_in["wu"], b_in["wd"], b_in["k"],
+                           expert_bias=b_in["bias"])
+        outs.append((oa, ob))
+    torch.cuda.synchronize()
+    for oa, ob in outs:
+        assert torch.equal(oa, ra) and torch.equal(ob, rb)

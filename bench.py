@@ -173,6 +173,9 @@ def main():
     ap.add_argument("--shared-expert", action="store_true",
                     help="also time the step with a DeepSeek-style always-on shared expert (seeded weights, "
                          "moe_fused_forward_shared from the same logits) and check it on sampled tokens; fp16 only")
+    ap.add_argument("--ep-shards", type=int, default=0,
+                    help="also time one expert-parallel shard (experts [0, E/G), moe_fused_forward_shard) at its "
+                         "real shape: the work one GPU of G does between dispatch and combine; fp16 only")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -387,6 +390,31 @@ def main():
             shared["within_rtol2e-2_atol1e-2"] = bool(torch.isfinite(got).all()) and \
                 bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
 
+    ep = None
+    if args.ep_shards > 1 and not w8:
+        G = args.ep_shards
+        if E % G:
+            raise SystemExit(f"--ep-shards {G} must divide E={E}")
+        n = E // G
+        sbm = args.block_m or int(L.moe_pick_block_m(T, E, k))
+        ews = torch.empty(int(L.moe_fused_shard_workspace_bytes(T, H, I, E, k, n, sbm)), dtype=torch.uint8,
+                          device=dev)
+        eout = torch.empty_like(out)
+        eargs = head + [P(inp[w_].data_ptr()) for w_ in ("wg", "wu", "wd")] + \
+            [P(eout.data_ptr()), T, H, I, E, k, 0, n, sbm, P(ews.data_ptr()), ews.numel(), P(0), P(0), stream, P(0)]
+        e_ms = timed(L.moe_fused_forward_shard, eargs, "moe_fused_forward_shard")
+        local = ids_np < n
+        lp = int(local.sum())
+        lt = int(np.unique(ids_np[local]).size)
+        e_flops = 6.0 * H * I * lp
+        e_bytes = lt * 3.0 * H * I * 2 + T * H * 2 * 2 + T * E * 4 + T * k * 8
+        ep = {"shards": G, "experts_local": n, "pairs_local": lp, "experts_touched_local": lt,
+              "shard_ms": round(e_ms, 4), "tflops": round(e_flops / (e_ms * 1e-3) / 1e12, 2),
+              "gb_per_s": round(e_bytes / (e_ms * 1e-3) / 1e9, 1),
+              "frac_of_roofline_time": round(max(e_flops / (PEAK_F16_TFLOPS * 1e12),
+                                                 e_bytes / (PEAK_HBM_GBS * 1e9)) / (e_ms * 1e-3), 4),
+              "shards_x_shard_ms_over_full_ms": round(G * e_ms / ms, 3)}
+
     copy_gbs = None
     if args.calib_copy:
         n = 1 << 29  # 1 GiB of fp16 read + 1 GiB written per copy
@@ -457,6 +485,8 @@ def main():
         res["router"] = router
     if shared is not None:
         res["shared_expert"] = shared
+    if ep is not None:
+        res["ep_shard"] = ep
     print(json.dumps(res), flush=True)
 
 

@@ -196,6 +196,26 @@ int moe_fused_forward_ex(const void* x, const float* logits, const void* w_route
                          int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                          void* const* stage_events);
 
+/* moe_fused_forward_shard: one expert-parallel shard of moe_fused_forward.
+ * Routing runs over all E_total experts (logits fp32 [T, E_total], bias
+ * [E_total] or NULL); the weights hold only experts [expert_begin,
+ * expert_begin + E_local) ([E_local, I, H] / [E_local, H, I]); out receives
+ * this shard's partial sum, out[t] = sum over choices j of token t routed to
+ * the shard of w_tj * y_tj (0 for tokens with none), so the partial outputs of
+ * shards covering all experts sum to the full layer.  topk_ids_out /
+ * topk_weights_out are the global [T, k] routing.  fp16, no shared expert;
+ * workspace moe_fused_shard_workspace_bytes bytes.  What one GPU of an
+ * expert-parallel layout computes between the token dispatch and the combine
+ * exchanges (which this library does not do).  No counterpart in the
+ * reference (problem_detail.json:18, :30: one device, no sharding). */
+int64_t moe_fused_shard_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
+                                        int64_t E_local, int64_t block_m);
+int moe_fused_forward_shard(const void* x, const float* logits, const float* bias, const void* w_gate,
+                            const void* w_up, const void* w_down, void* out, int64_t T, int64_t H, int64_t I,
+                            int64_t E_total, int64_t k, int64_t expert_begin, int64_t E_local, int64_t block_m,
+                            void* workspace, int64_t workspace_bytes, int32_t* topk_ids_out,
+                            float* topk_weights_out, void* stream, void* const* stage_events);
+
 /* ------------------------------------------------------------------------
  * W8A8.  moe_quantize_rows_w8: per-row symmetric int8 of an fp16 [R, K]
  * matrix: scale = max|row|/127, q = clamp(trunc(w*(127/max|row|) +- 0.5),

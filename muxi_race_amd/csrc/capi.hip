@@ -222,17 +222,25 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
 static int fused_common(int qt, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
                         const void* wd, const float* sd, const void* wg_s, const void* wu_s,
-                        const void* wd_s, const int64_t* wstr, void* out, int64_t T, int64_t H,
+                        const void* wd_s, const int64_t* wstr, int64_t e_begin, int64_t E_route,
+                        void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                         int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
                         void* const* ev) {
   const bool w8 = qt != moe::kQF16;  // 8-bit operands: int8 or fp8
+  // expert shard: routing over E_route experts, this call's weights hold
+  // experts [e_begin, e_begin + E); only their pairs are computed and summed
+  const bool shard = E_route > 0;
+  if (!shard) E_route = E;
+  if (shard && (e_begin < 0 || E <= 0 || e_begin + E > E_route || w_router || wg_s || wu_s || wd_s))
+    return fail(MOE_ERR_INVALID_ARG, "expert shard [%lld, %lld) of %lld experts (logits only, no shared expert)",
+                (long long)e_begin, (long long)(e_begin + E), (long long)E_route);
   const bool shared = wg_s || wu_s || wd_s;
   if (shared && (w8 || !wg_s || !wu_s || !wd_s))
     return fail(w8 ? MOE_ERR_UNSUPPORTED : MOE_ERR_INVALID_ARG, w8 ? "the shared expert is supported on the fp16 path" : "null pointer argument");
   const int64_t Ee = E + (shared ? 1 : 0), ke = k + (shared ? 1 : 0);  // experts / choices incl. the shared one
-  if (block_m == 0) block_m = pick_bm(T, Ee, ke);
-  int rc = check_dims(T, H, I, Ee, ke, block_m);
+  if (block_m == 0) block_m = pick_bm(T, shard ? E_route : Ee, ke);
+  int rc = check_dims(T, H, I, shard ? E_route : Ee, ke, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
   if (!x || (!logits && !w_router) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
@@ -272,11 +280,11 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   mark(0);
   if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
     if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s, e_shared), "router"))) return rc;
-  } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E, (int)k, ids, wts, s, e_shared), "route_topk"))) {
+  } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E_route, (int)k, ids, wts, s, e_shared), "route_topk"))) {
     return rc;
   }
   mark(1);
-  if ((rc = check_launch(moe::launch_align(ids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s), "align"))) return rc;
+  if ((rc = check_launch(moe::launch_align(ids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s, (int)e_begin), "align"))) return rc;
   mark(2);
   if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, ws + L.xq, (float*)(ws + L.sx), qt, s), "quantize_x"))) return rc;
   mark(3);
@@ -328,7 +336,8 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.I = I;
   if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, qt, true, rows / block_m, s), "stage2"))) return rc;
   mark(5);
-  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s), "combine");
+  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s, shard ? ids : nullptr, (int)e_begin, (int)E),
+                    "combine");
   mark(6);
   return rc;
 }
@@ -338,7 +347,7 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias, con
                       int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                       int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                       void* stream) {
-  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -355,7 +364,7 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
                              int64_t workspace_bytes, int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream) {
   if (!w_router && T > 0) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
-  return fused_common(moe::kQF16, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, nullptr, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -376,7 +385,7 @@ int moe_fused_forward_shared(const void* x, const float* logits, const void* w_r
   if (T > 0 && (!logits) == (!w_router)) return fail(MOE_ERR_INVALID_ARG, "give exactly one of logits and w_router");
   if (T > 0 && (!w_gate_shared || !w_up_shared || !w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   return fused_common(moe::kQF16, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
-                      w_gate_shared, w_up_shared, w_down_shared, nullptr, out, T, H, I, E, k, block_m, workspace,
+                      w_gate_shared, w_up_shared, w_down_shared, nullptr, 0, 0, out, T, H, I, E, k, block_m, workspace,
                       workspace_bytes, topk_ids_out, topk_weights_out, stream, nullptr);
 }
 
@@ -398,8 +407,26 @@ int moe_fused_forward_ex(const void* x, const float* logits, const void* w_route
   const bool any = w_gate_shared || w_up_shared || w_down_shared;
   if (T > 0 && any && !(w_gate_shared && w_up_shared && w_down_shared)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   return fused_common(moe::kQF16, x, logits, w_router, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
-                      w_gate_shared, w_up_shared, w_down_shared, weight_strides, out, T, H, I, E, k, block_m,
+                      w_gate_shared, w_up_shared, w_down_shared, weight_strides, 0, 0, out, T, H, I, E, k, block_m,
                       workspace, workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
+}
+
+int64_t moe_fused_shard_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
+                                        int64_t E_local, int64_t block_m) {
+  if (T < 0 || H <= 0 || I <= 0 || E_total <= 0 || E_local <= 0 || k <= 0) return 0;
+  if (block_m == 0) block_m = pick_bm(T, E_total, k);
+  return fused_layout(T, H, I, E_local, k, block_m, false).total;
+}
+
+int moe_fused_forward_shard(const void* x, const float* logits, const float* bias, const void* w_gate,
+                            const void* w_up, const void* w_down, void* out, int64_t T, int64_t H, int64_t I,
+                            int64_t E_total, int64_t k, int64_t expert_begin, int64_t E_local, int64_t block_m,
+                            void* workspace, int64_t workspace_bytes, int32_t* topk_ids_out,
+                            float* topk_weights_out, void* stream, void* const* stage_events) {
+  if (E_total <= 0) return fail(MOE_ERR_INVALID_ARG, "E_total=%lld", (long long)E_total);
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, expert_begin, E_total, out, T, H, I, E_local, k, block_m, workspace,
+                      workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
 }
 
 int moe_fused_forward_events(const void* x, const float* logits, const float* bias,
@@ -408,7 +435,7 @@ int moe_fused_forward_events(const void* x, const float* logits, const float* bi
                              int64_t block_m, void* workspace, int64_t workspace_bytes,
                              int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                              void* const* stage_events) {
-  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }
@@ -439,7 +466,7 @@ int moe_fused_forward_fp8(const void* x, const float* logits, const float* bias,
                           int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                           void* const* stage_events) {
   return fused_common(moe::kQF8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr,
-                      nullptr, nullptr, nullptr, out, T, H, I, E, k, block_m, workspace, workspace_bytes,
+                      nullptr, nullptr, nullptr, 0, 0, out, T, H, I, E, k, block_m, workspace, workspace_bytes,
                       topk_ids_out, topk_weights_out, stream, stage_events);
 }
 
@@ -449,7 +476,7 @@ int moe_fused_forward_w8a8(const void* x, const float* logits, const float* bias
                            void* out, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                            int64_t block_m, void* workspace, int64_t workspace_bytes,
                            int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
-  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, 0, 0, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, nullptr);
 }
@@ -461,7 +488,7 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   int64_t block_m, void* workspace, int64_t workspace_bytes,
                                   int32_t* topk_ids_out, float* topk_weights_out, void* stream,
                                   void* const* stage_events) {
-  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, out,
+  return fused_common(moe::kQI8, x, logits, nullptr, bias, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, nullptr, nullptr, nullptr, nullptr, 0, 0, out,
                       T, H, I, E, k, block_m, workspace, workspace_bytes, topk_ids_out,
                       topk_weights_out, stream, stage_events);
 }

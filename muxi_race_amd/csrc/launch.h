@@ -88,9 +88,11 @@ inline int align_pairs_per_group(int P, int groups, int nw) {
   const int per = (P + groups - 1) / groups;
   return (per + 64 * nw - 1) / (64 * nw) * (64 * nw);
 }
-hipError_t launch_align(const int32_t* ids, int P, int E, int block_m, int32_t* sorted_ids,
+// e_off: pairs are bucketed by id - e_off; ids outside [e_off, e_off + E)
+// are dropped (an expert shard of a wider routing).
+hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
-                        int32_t* whist, hipStream_t stream);
+                        int32_t* whist, hipStream_t stream, int e_off = 0);
 // Router GEMM (x . w_router^T, K split in router_splits parts) + routing of
 // the summed partials; `part` holds router_partial_floats fp32, `logits`
 // (fp32 [T, E]) may be null.
@@ -99,8 +101,9 @@ int64_t router_partial_floats(int64_t T, int64_t H, int64_t E);
 hipError_t launch_router(const void* x, const void* w_router, const float* bias, int T, int64_t H, int E,
                          int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t stream,
                          int e_shared = -1);
+// ids (may be null): sum only pairs whose expert is in [e_lo, e_lo + e_n).
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
-                          hipStream_t stream);
+                          hipStream_t stream, const int32_t* ids = nullptr, int e_lo = 0, int e_n = 0);
 // Per-row 8-bit quantisation of an fp16 [R, K] matrix to the format qt
 // (kQI8 or kQF8): codes into q, amax / qmax into scale.
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,

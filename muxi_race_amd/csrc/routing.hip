@@ -69,7 +69,7 @@ constexpr int kAlignUnroll = 8;
 
 // count: the wave's private histogram hw[E] (no other wave touches it)
 __device__ __forceinline__ void align_count_range(const int32_t* __restrict__ ids, int p0, int p1, int E,
-                                                  int nbits, int* hw) {
+                                                  int e_off, int nbits, int* hw) {
   const int l = lane_id();
   for (int i = l; i < E; i += 64) hw[i] = 0;
   const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
@@ -82,9 +82,9 @@ __device__ __forceinline__ void align_count_range(const int32_t* __restrict__ id
     }
 #pragma unroll
     for (int u = 0; u < kAlignUnroll; ++u) {
-      int e = ev[u];
-      const bool ok = (unsigned)e < (unsigned)E;
-      if (!ok) e = 0;
+      const unsigned ue = (unsigned)ev[u] - (unsigned)e_off;  // expert relative to the first one kept
+      const bool ok = ue < (unsigned)E;
+      const int e = ok ? (int)ue : 0;
       const uint64_t same = same_expert_mask(e, ok, nbits);
       if (ok && __popcll(same & lt_mask) == 0) hw[e] += __popcll(same);
     }
@@ -93,7 +93,7 @@ __device__ __forceinline__ void align_count_range(const int32_t* __restrict__ id
 
 // place, in pair order: pair p goes to hw[e] + rank, then the cursor advances
 __device__ __forceinline__ void align_place_range(const int32_t* __restrict__ ids, int p0, int p1, int E,
-                                                  int nbits, int* hw, int32_t* __restrict__ sorted_ids) {
+                                                  int e_off, int nbits, int* hw, int32_t* __restrict__ sorted_ids) {
   const int l = lane_id();
   const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
   for (int base = p0; base < p1; base += 64 * kAlignUnroll) {
@@ -106,9 +106,9 @@ __device__ __forceinline__ void align_place_range(const int32_t* __restrict__ id
 #pragma unroll
     for (int u = 0; u < kAlignUnroll; ++u) {
       const int p = base + 64 * u + l;
-      int e = ev[u];
-      const bool ok = (unsigned)e < (unsigned)E;
-      if (!ok) e = 0;
+      const unsigned ue = (unsigned)ev[u] - (unsigned)e_off;
+      const bool ok = ue < (unsigned)E;
+      const int e = ok ? (int)ue : 0;
       const uint64_t same = same_expert_mask(e, ok, nbits);
       const int rank = __popcll(same & lt_mask);
       if (ok) {
@@ -184,7 +184,7 @@ __device__ __forceinline__ int bits_for(int E) {
 // prefix per expert and the expert scan; 3. place; 4. fill.
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void align_kernel(
-    const int32_t* __restrict__ ids, int P, int E, int BM, int32_t* __restrict__ sorted_ids,
+    const int32_t* __restrict__ ids, int P, int E, int e_off, int BM, int32_t* __restrict__ sorted_ids,
     int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
     int32_t* __restrict__ gpo) {
   extern __shared__ int sm[];
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(64 * NW) void align_kernel(
   const int R = ((P + NW - 1) / NW + 63) / 64 * 64;
   const int p0 = w * R, p1 = min(P, p0 + R);
   int* hw = hist + w * E;
-  align_count_range(ids, p0, p1, E, nbits, hw);
+  align_count_range(ids, p0, p1, E, e_off, nbits, hw);
   __syncthreads();
   for (int e = tid; e < E; e += 64 * NW) {
     int run = 0;
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(64 * NW) void align_kernel(
   for (int e = tid; e < E; e += 64 * NW)
     for (int v = 0; v < NW; ++v) hist[v * E + e] += pstart[e];
   __syncthreads();
-  align_place_range(ids, p0, p1, E, nbits, hw, sorted_ids);
+  align_place_range(ids, p0, p1, E, e_off, nbits, hw, sorted_ids);
   align_fill(pstart, tot, E, BM, P, w, NW, sorted_ids, block_expert);
 }
 
@@ -224,14 +224,14 @@ __global__ __launch_bounds__(64 * NW) void align_kernel(
 // Pair order within an expert, hence the output, is the one-workgroup kernel's.
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void align_count_kernel(const int32_t* __restrict__ ids, int P, int E,
-                                                              int RW, int32_t* __restrict__ whist) {
+                                                              int e_off, int RW, int32_t* __restrict__ whist) {
   extern __shared__ int sm[];
   int* hist = sm;  // [NW][E]
   const int tid = threadIdx.x, w = tid >> 6;
   const int g0 = blockIdx.x * RW, g1 = min(P, g0 + RW);
   const int R = RW / NW;
   const int p0 = min(g1, g0 + w * R), p1 = min(g1, p0 + R);
-  align_count_range(ids, p0, p1, E, bits_for(E), hist + w * E);
+  align_count_range(ids, p0, p1, E, e_off, bits_for(E), hist + w * E);
   __syncthreads();
   for (int e = tid; e < E; e += 64 * NW) {
     int run = 0;
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(64 * NW) void align_count_kernel(const int32_t* __r
 
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void align_place_kernel(
-    const int32_t* __restrict__ ids, int P, int E, int BM, int RW, const int32_t* __restrict__ whist,
+    const int32_t* __restrict__ ids, int P, int E, int e_off, int BM, int RW, const int32_t* __restrict__ whist,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ block_expert, int32_t* __restrict__ gs,
     int32_t* __restrict__ go, int32_t* __restrict__ gpo) {
   extern __shared__ int sm[];
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64 * NW) void align_place_kernel(
   const int p0 = min(g1, g0 + w * R), p1 = min(g1, p0 + R);
   const int nbits = bits_for(E);
   int* hw = hist + w * E;
-  align_count_range(ids, p0, p1, E, nbits, hw);
+  align_count_range(ids, p0, p1, E, e_off, nbits, hw);
   __syncthreads();
   if (w == 0) align_expert_scan(tot, E, BM, pstart, g == 0, gs, go, gpo);
   __syncthreads();
@@ -280,13 +280,13 @@ __global__ __launch_bounds__(64 * NW) void align_place_kernel(
     }
   }
   __syncthreads();
-  align_place_range(ids, p0, p1, E, nbits, hw, sorted_ids);
+  align_place_range(ids, p0, p1, E, e_off, nbits, hw, sorted_ids);
   align_fill(pstart, tot, E, BM, P, g * NW + w, G * NW, sorted_ids, block_expert);
 }
 
 hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorted_ids,
                         int32_t* block_expert, int32_t* gs, int32_t* go, int32_t* gpo,
-                        int32_t* whist, hipStream_t s) {
+                        int32_t* whist, hipStream_t s, int e_off) {
   // 16 waves while the histograms fit 48 KiB of LDS, else 8 (E <= 1024)
   const bool w16 = 16 * E <= 12288;
   const int G = align_groups(P);
@@ -296,23 +296,23 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
     const size_t lds1 = sizeof(int) * ((size_t)NW * E);
     const size_t lds2 = sizeof(int) * ((size_t)NW * E + 3 * (size_t)E + 1);
     if (w16) {
-      hipLaunchKernelGGL(align_count_kernel<16>, dim3(G), dim3(1024), lds1, s, ids, P, E, RW, whist);
-      hipLaunchKernelGGL(align_place_kernel<16>, dim3(G), dim3(1024), lds2, s, ids, P, E, BM, RW, whist,
+      hipLaunchKernelGGL(align_count_kernel<16>, dim3(G), dim3(1024), lds1, s, ids, P, E, e_off, RW, whist);
+      hipLaunchKernelGGL(align_place_kernel<16>, dim3(G), dim3(1024), lds2, s, ids, P, E, e_off, BM, RW, whist,
                          sorted_ids, block_expert, gs, go, gpo);
     } else {
-      hipLaunchKernelGGL(align_count_kernel<8>, dim3(G), dim3(512), lds1, s, ids, P, E, RW, whist);
-      hipLaunchKernelGGL(align_place_kernel<8>, dim3(G), dim3(512), lds2, s, ids, P, E, BM, RW, whist,
+      hipLaunchKernelGGL(align_count_kernel<8>, dim3(G), dim3(512), lds1, s, ids, P, E, e_off, RW, whist);
+      hipLaunchKernelGGL(align_place_kernel<8>, dim3(G), dim3(512), lds2, s, ids, P, E, e_off, BM, RW, whist,
                          sorted_ids, block_expert, gs, go, gpo);
     }
     return hipGetLastError();
   }
   if (w16) {
     const size_t lds = sizeof(int) * (16 * (size_t)E + 2 * (size_t)E + 1);
-    hipLaunchKernelGGL(align_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, BM, sorted_ids,
+    hipLaunchKernelGGL(align_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, e_off, BM, sorted_ids,
                        block_expert, gs, go, gpo);
   } else {
     const size_t lds = sizeof(int) * (8 * (size_t)E + 2 * (size_t)E + 1);
-    hipLaunchKernelGGL(align_kernel<8>, dim3(1), dim3(512), lds, s, ids, P, E, BM, sorted_ids,
+    hipLaunchKernelGGL(align_kernel<8>, dim3(1), dim3(512), lds, s, ids, P, E, e_off, BM, sorted_ids,
                        block_expert, gs, go, gpo);
   }
   return hipGetLastError();
@@ -322,10 +322,13 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
 // Combine: out[t, :] = sum_j y_pair[t*k + j, :], fp32 in choice order -> fp16.
 // One thread per 8 output columns.  The k rows are loaded in batches of 8
 // before they are summed (in choice order), so each thread keeps several loads
-// in flight; y_pair is read once, so the loads are non-temporal.
+// in flight; y_pair is read once, so the loads are non-temporal.  With `ids`
+// (an expert shard), only pairs routed to experts [e_lo, e_lo + e_n) are
+// summed: the others' rows were never written.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y, int64_t T,
-                                                      int64_t H, int k, _Float16* __restrict__ out) {
+                                                      int64_t H, int k, _Float16* __restrict__ out,
+                                                      const int32_t* __restrict__ ids, int e_lo, int e_n) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t cpr = H / 8;
   if (idx >= T * cpr) return;
@@ -335,12 +338,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   constexpr int kBatch = 8;
   for (int j0 = 0; j0 < k; j0 += kBatch) {
     f16x8 v[kBatch];
+    bool in[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (j0 + u < k) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)(j0 + u) * H));
+      in[u] = j0 + u < k && (!ids || (unsigned)ids[t * k + j0 + u] - (unsigned)e_lo < (unsigned)e_n);
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (j0 + u < k) {
+      if (in[u]) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)(j0 + u) * H));
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (in[u]) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[q] += (float)v[u][q];
       }
@@ -352,12 +359,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
 }
 
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
-                          hipStream_t s) {
+                          hipStream_t s, const int32_t* ids, int e_lo, int e_n) {
   const int64_t n = T * (H / 8);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      reinterpret_cast<const _Float16*>(y_pair), T, H, k,
-                     reinterpret_cast<_Float16*>(out));
+                     reinterpret_cast<_Float16*>(out), ids, e_lo, e_n);
   return hipGetLastError();
 }
 

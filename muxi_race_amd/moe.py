@@ -264,7 +264,7 @@ def quantize_w8a8_weights(w_gate, w_up, w_down, fmt: str = "int8") -> W8A8Weight
 # ---------------------------------------------------------------------------
 def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
               expert_bias=None, w8a8: W8A8Weights | None = None, block_m: int = 0, out=None,
-              return_routing: bool = False, router_weight=None, shared_expert=None):
+              return_routing: bool = False, router_weight=None, shared_expert=None, expert_range=None):
     """Full MoE FFN: softmax/top-k/renormalise routing, expert SwiGLU MLPs,
     routing-weighted combine.  hidden_states fp16 [T, H], router_logits fp32
     [T, E], w_gate/w_up fp16 [E, I, H], w_down fp16 [E, H, I] (or ``w8a8``
@@ -278,6 +278,10 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
     fp16 weights may be strided views (rows and experts apart, e.g. the two
     halves of a fused [E, 2I, H] gate/up tensor): w_gate and w_up share their
     strides, the shared expert's rows use the routed experts' row strides.
+    ``expert_range`` = (begin, count): one expert-parallel shard -- the logits
+    cover all experts, the (dense fp16) weights only experts [begin, begin +
+    count), and the result is this shard's partial sum (the shards' results
+    add up to the full layer); the routing returned is the global one.
     Returns fp16 [T, H] (and (ids, weights) when ``return_routing``)."""
     x = hidden_states
     _need(x, "hidden_states", (torch.float16,), 2)
@@ -297,6 +301,13 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
         E = router_logits.shape[1]
         if router_logits.shape[0] != T:
             raise ValueError("router_logits rows != tokens")
+    E_route = E
+    if expert_range is not None:
+        if router_weight is not None or w8a8 is not None or shared_expert is not None:
+            raise ValueError("expert_range takes router_logits and fp16 weights, without a shared expert")
+        e_begin, E = (int(v) for v in expert_range)
+        if e_begin < 0 or E < 1 or e_begin + E > E_route:
+            raise ValueError(f"expert_range {expert_range} outside the {E_route} routed experts")
     if w8a8 is None:
         for name, t in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down)):
             _need(t, name, (torch.float16,), 3, dev, strided_ok=True)
@@ -335,7 +346,7 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
             raise ValueError("shared expert rows must use the routed experts' row strides")
     if expert_bias is not None:
         _need(expert_bias, "expert_bias", (torch.float32,), 1, dev)
-        if expert_bias.numel() != E:
+        if expert_bias.numel() != E_route:
             raise ValueError("expert_bias must have E entries")
     if out is None:
         out = torch.empty((T, H), dtype=torch.float16, device=dev)
@@ -344,6 +355,19 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
         if tuple(out.shape) != (T, H):
             raise ValueError("out shape mismatch")
     L = lib()
+    if expert_range is not None:
+        if not (w_gate.is_contiguous() and w_up.is_contiguous() and w_down.is_contiguous()):
+            raise ValueError("expert_range takes dense weights")
+        bm = block_m or int(L.moe_pick_block_m(T, E_route, top_k))
+        ws = _workspace(dev, ("fused", False), L.moe_fused_shard_workspace_bytes(T, H, I, E_route, top_k, E, bm))
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev) if return_routing else None
+        wts = torch.empty((T, top_k), dtype=torch.float32, device=dev) if return_routing else None
+        with torch.cuda.device(dev):
+            rc = L.moe_fused_forward_shard(_ptr(x), _ptr(router_logits), _ptr(expert_bias), _ptr(w_gate),
+                                           _ptr(w_up), _ptr(w_down), _ptr(out), T, H, I, E_route, top_k, e_begin, E,
+                                           bm, _ptr(ws), ws.numel(), _ptr(ids), _ptr(wts), _stream(dev), None)
+        check(rc, "fused_moe")
+        return (out, (ids, wts)) if return_routing else out
     ncol = top_k + (shared_expert is not None)
     bm = block_m or int(L.moe_pick_block_m(T, E + (shared_expert is not None), ncol))
     if shared_expert is not None:

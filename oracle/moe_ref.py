@@ -189,7 +189,7 @@ def combine(y_pair: torch.Tensor, T: int, top_k: int) -> torch.Tensor:
 
 
 def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
-                      block_m: int = 128, *, return_aux=False, experts=None, shared=None):
+                      block_m: int = 128, *, return_aux=False, experts=None, shared=None, expert_range=None):
     """Full MoE: route -> align -> gather -> pre-routed MLP -> weighted combine.
 
     Returns float16 [T, H] (and the routing/alignment intermediates when
@@ -198,13 +198,26 @@ def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
     reference's own loop.  ``shared`` = (w_gate_s [I, H], w_up_s [I, H],
     w_down_s [H, I]) adds an always-on expert: expert E, appended to every
     token as choice k with weight 1 (outside the top-k renormalisation), so
-    the routing has k + 1 columns.
+    the routing has k + 1 columns.  ``expert_range`` = (begin, count): an
+    expert shard -- routing over all logits columns, weights of experts
+    [begin, begin + count) only, and the sum over each token's choices routed
+    there (other choices go to an appended all-zero expert with weight 0, which
+    adds exactly 0).
     """
     x = _as_t(x)
     T, H = x.shape
     E = int(w_gate.shape[0])
     ids, w = route_topk(_as_t(logits).float().numpy(), top_k,
                         None if bias is None else _as_t(bias).float().numpy())
+    ids_global = ids
+    if expert_range is not None:
+        b, n = expert_range
+        mine = (ids >= b) & (ids < b + n)
+        ids = np.where(mine, ids - b, n).astype(np.int32)
+        w = np.where(mine, w, np.float32(0)).astype(np.float32)
+        z = lambda t: torch.cat([_as_t(t), torch.zeros_like(_as_t(t)[:1])])
+        w_gate, w_up, w_down = z(w_gate), z(w_up), z(w_down)
+        E = n + 1
     if shared is not None:
         ids = np.concatenate([ids, np.full((T, 1), E, np.int32)], axis=1)
         w = np.concatenate([w, np.ones((T, 1), np.float32)], axis=1)
@@ -229,7 +242,7 @@ def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
     y_pair[vs[mask]] = y_sorted[mask]
     out = combine(y_pair, T, top_k).to(torch.float16)
     if return_aux:
-        return out, dict(ids=ids, weights=w, **al)
+        return out, dict(ids=ids if expert_range is None else ids_global, weights=w, **al)
     return out
 
 

@@ -212,3 +212,36 @@ def test_shared_expert_closed_forms(rng):
         g, u = xd @ sg.double().T, xd @ su.double().T
         dense = (torch.sigmoid(g) * g * u) @ sd.double().T
         torch.testing.assert_close(both.double() - routed.double(), dense, rtol=2e-3, atol=3e-3)
+
+
+def test_expert_shards_closed_forms(rng):
+    """Expert shards: one shard over all experts is the full layer exactly; the
+    partial outputs of disjoint shards covering all experts sum to the full
+    layer (fp16 rounding of each part aside); a shard owning none of a
+    token's choices gives that token 0."""
+    T, H, I, E, k = 33, 32, 16, 8, 3
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16))
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32))
+    wg = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wu = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wd = torch.from_numpy((rng.standard_normal((E, H, I)) * 0.2).astype(np.float16))
+    full, aux = fused_moe_forward(x, logits, wg, wu, wd, k, bias, return_aux=True)
+    whole = fused_moe_forward(x, logits, wg, wu, wd, k, bias, expert_range=(0, E))
+    assert torch.equal(whole, full)
+    parts = [fused_moe_forward(x, logits, wg[b:b + n], wu[b:b + n], wd[b:b + n], k, bias, expert_range=(b, n))
+             for b, n in ((0, 3), (3, 1), (4, 4))]
+    torch.testing.assert_close(sum(p.double() for p in parts), full.double(), rtol=0, atol=3e-3)
+    ids = aux["ids"]
+    none_in_1 = ~(ids == 3).any(axis=1)            # tokens without a choice of expert 3
+    assert (parts[1][torch.from_numpy(none_in_1)] == 0).all()
+    # a shard = the dense per-token sum over its own experts
+    exp = torch.zeros(T, H, dtype=torch.float64)
+    _, w = route_topk(logits.numpy(), k, bias.numpy())
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            if 4 <= e < 8:
+                g, u = wg[e].double() @ x[t].double(), wu[e].double() @ x[t].double()
+                exp[t] += float(w[t, j]) * (wd[e].double() @ (torch.sigmoid(g) * g * u))
+    torch.testing.assert_close(parts[2].double(), exp, rtol=2e-3, atol=2e-3)

@@ -101,3 +101,31 @@ def test_two_streams_do_not_share_scratch():
     torch.cuda.synchronize()
     for oa, ob in outs:
         assert torch.equal(oa, ra) and torch.equal(ob, rb)
+
+
+def _random_case(T, H, I, E, k, seed, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    return dict(x=torch.randn(T, H, generator=g).half().cuda(), logits=torch.randn(T, E, generator=g).cuda(),
+                bias=(torch.randn(E, generator=g) * 0.5).cuda() if bias else None,
+                wg=(torch.randn(E, I, H, generator=g) * 0.05).half().cuda(),
+                wu=(torch.randn(E, I, H, generator=g) * 0.05).half().cuda(),
+                wd=(torch.randn(E, H, I, generator=g) * 0.05).half().cuda(), k=k, T=T, H=H, I=I, E=E)
+
+
+@pytest.mark.parametrize("T,H,I,E,k", [
+    (1, 128, 128, 1, 1),        # smallest legal problem
+    (3, 128, 256, 1024, 32),    # widest routing: E = 1024 experts, k = 32 choices
+    (257, 256, 128, 32, 32),    # every token takes every expert (k = E)
+    (129, 384, 640, 5, 3),      # odd expert count, H and I not powers of two
+])
+def test_extreme_shapes(T, H, I, E, k):
+    _check(_random_case(T, H, I, E, k, T + E), what=f"T={T} H={H} I={I} E={E} k={k}")
+
+
+def test_empty_batch():
+    from muxi_race_amd import fused_moe
+    inp = _random_case(1, 128, 128, 4, 2, 5)
+    x = inp["x"][:0]
+    out, (ids, w) = fused_moe(x, inp["logits"][:0], inp["wg"], inp["wu"], inp["wd"], 2, return_routing=True)
+    torch.cuda.synchronize()
+    assert out.shape == (0, 128) and ids.shape == (0, 2) and w.shape == (0, 2)

@@ -19,6 +19,11 @@
  *   moe_quantize_rows_w8 <- W8A8 weight/activation quantisers,
  *                           xpuoj_data/submission_v321_int8_fixed.py:160-227
  *   moe_fused_forward_w8a8 <- W8A8 pipeline, submission_v321_int8_fixed.py:421-506
+ * Extensions with no reference counterpart (each documented below): the
+ * router GEMM (moe_route_hidden, moe_fused_forward_hidden), the shared expert
+ * (moe_fused_forward_shared), strided weights (moe_fused_forward_ex), one
+ * expert-parallel shard (moe_fused_forward_shard) and the fp8 variant
+ * (moe_quantize_rows_fp8, moe_fused_forward_fp8).
  */
 #ifndef MOE_GFX950_H
 #define MOE_GFX950_H

@@ -1,13 +1,16 @@
 // Grouped expert GEMMs for gfx950: Stage 1 (gate/up + SiLU*up) and Stage 2
-// (down projection * routing weight), fp16 MFMA (v_mfma_f32_32x32x16_f16) and
-// int8 MFMA (v_mfma_i32_32x32x32_i8).
+// (down projection * routing weight) on fp16 MFMA (v_mfma_f32_32x32x16_f16),
+// int8 MFMA (v_mfma_i32_32x32x32_i8) or fp8 MFMA (v_mfma_f32_32x32x64_f8f6f4,
+// OCP e4m3).
 //
 // Reference algorithm: 初审材料/源代码/submission.py Stage1 family (:136-247,
 // :1391-1635) and Stage2 family (:655-795, :1132-1378); base form
 // xpuoj_data/submission.py:31-129 and :253-331.  The tiling here is this
-// build's own: a 256-thread workgroup computes a BM x 128 output tile (Stage 1:
-// for gate and up at once, sharing the token tile); K advances 128 bytes per
-// step through an S-stage ring of XOR-swizzled LDS tiles filled by direct
+// build's own.  A workgroup (4 waves for 32/64-row tiles, 8 for 128-row ones)
+// computes a BM x 128 output tile (Stage 1: gate and up at once, sharing the
+// token tile; Stage 2 of 128-row tiles: 256 features), or a paired 2*BM x 64
+// (x 128) item for experts with several blocks.  K advances 128 bytes per step
+// through an S-stage ring of XOR-swizzled LDS tiles filled by direct
 // global->LDS loads (global_load_lds_dwordx4), so S-2 steps of loads stay in
 // flight behind the MFMAs of the current step, with one barrier per step.
 #include "launch.h"

@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--shared-expert", action="store_true",
                     help="also time the step with a DeepSeek-style always-on shared expert (seeded weights, "
                          "moe_fused_forward_shared from the same logits) and check it on sampled tokens; fp16 only")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the step captured once in a HIP graph (torch.cuda.graph) and replayed")
     ap.add_argument("--ep-shards", type=int, default=0,
                     help="also time one expert-parallel shard (experts [0, E/G), moe_fused_forward_shard) at its "
                          "real shape: the work one GPU of G does between dispatch and combine; fp16 only")
@@ -390,6 +392,31 @@ def main():
             shared["within_rtol2e-2_atol1e-2"] = bool(torch.isfinite(got).all()) and \
                 bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())
 
+    graph = None
+    if args.graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            check(fwd(*cargs[:-1], P(side.cuda_stream)), name)  # same buffers, on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        ref_out = out.clone()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            check(fwd(*cargs[:-1], P(torch.cuda.current_stream().cuda_stream)), name)
+        for _ in range(args.warmup):
+            gr.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(args.steps):
+            gr.replay()
+        b.record()
+        torch.cuda.synchronize()
+        g_ms = a.elapsed_time(b) / args.steps
+        graph = {"graph_ms_per_step": round(g_ms, 4), "eager_ms_per_step": round(ms, 4),
+                 "replay_equals_eager": bool(torch.equal(out, ref_out))}
+
     ep = None
     if args.ep_shards > 1 and not w8:
         G = args.ep_shards
@@ -487,6 +514,8 @@ def main():
         res["shared_expert"] = shared
     if ep is not None:
         res["ep_shard"] = ep
+    if graph is not None:
+        res["graph"] = graph
     print(json.dumps(res), flush=True)
 
 

@@ -1,0 +1,59 @@
+"""The fused forward issues no memset and no allocation inside the library, so
+a caller can capture it in a HIP graph (torch.cuda.graph).  Each case is
+captured once and replayed several times with unrelated eager work and
+synchronisations between replays; every replay must equal the eager result
+bitwise."""
+import pytest
+import torch
+
+from _cases import moe_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _replays_match(fn, n=3):
+    eager = fn().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the capture stream's workspace outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    noise = torch.randn(1024, 1024, device="cuda")
+    for i in range(n):
+        _ = noise @ noise  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager result"
+
+
+@pytest.mark.parametrize("name", ["small", "decode"])
+def test_fp16_forward_replays(name):
+    from muxi_race_amd import fused_moe
+    inp = moe_inputs(name, 101)
+    _replays_match(lambda: fused_moe(inp["x"], inp["logits"], inp["wg"], inp["wu"], inp["wd"], inp["k"],
+                                     expert_bias=inp["bias"]))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_8bit_forward_replays(fmt):
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    inp = moe_inputs("small", 102, T=300)
+    qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt=fmt)
+    _replays_match(lambda: fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], w8a8=qw))
+
+
+def test_router_and_shared_expert_replays():
+    from muxi_race_amd import fused_moe
+    inp = moe_inputs("decode", 103)
+    g = torch.Generator(device="cuda").manual_seed(103)
+    H, I, E = inp["H"], inp["I"], inp["E"]
+    wr = (torch.randn((E, H), generator=g, device="cuda") / H ** 0.5).half()
+    sh = [torch.randn(s, generator=g, device="cuda", dtype=torch.float16) * 0.02 for s in ((I, H), (I, H), (H, I))]
+    _replays_match(lambda: fused_moe(inp["x"], None, inp["wg"], inp["wu"], inp["wd"], inp["k"],
+                                     expert_bias=inp["bias"], router_weight=wr, shared_expert=sh))

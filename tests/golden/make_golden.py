@@ -6,7 +6,9 @@ The reference commits no golden tensors (its harness writes .pt files at run
 time, xpuoj_data/remote_bench.py:254-257), so these fixtures hold seeded
 inputs and the CPU oracle's outputs for small cases of each path: the
 pre-routed operator on the problem_detail.json:40 layout (an empty expert and
-a two-block expert added), the full fused MoE with an expert bias, and W8A8.
+a two-block expert added), the full fused MoE with an expert bias, and W8A8;
+and, for the paths beyond the reference's operator, fp8 W8A8 codes and output,
+the router GEMM, the shared expert and an expert-parallel shard.
 """
 from pathlib import Path
 import sys
@@ -17,7 +19,7 @@ import torch
 ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 from oracle import (fused_moe_forward, metadata_from_group_sizes, prerouted_forward,  # noqa: E402
-                    quantize_rows_int8, route_topk, w8a8_forward)
+                    quantize_rows_fp8, quantize_rows_int8, route_topk, router_logits, w8a8_forward)
 
 OUT = Path(__file__).resolve().parent
 
@@ -61,9 +63,40 @@ def fused():
                         q_gate=qg, s_gate=sg)
 
 
+def extensions():
+    rng = np.random.default_rng(42)
+    T, H, I, E, k = 48, 256, 128, 8, 2
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    bias = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    wr = (rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float16)
+    wg = (rng.standard_normal((E, I, H)) * 0.05).astype(np.float16)
+    wu = (rng.standard_normal((E, I, H)) * 0.05).astype(np.float16)
+    wd = (rng.standard_normal((E, H, I)) * 0.05).astype(np.float16)
+    sg = (rng.standard_normal((I, H)) * 0.05).astype(np.float16)
+    su = (rng.standard_normal((I, H)) * 0.05).astype(np.float16)
+    sd = (rng.standard_normal((H, I)) * 0.05).astype(np.float16)
+    t = torch.from_numpy
+    logits = router_logits(x, wr)                      # fp32 [T, E] from the router GEMM
+    ids, w = route_topk(logits, k, bias)
+    out_router = fused_moe_forward(t(x), t(logits), t(wg), t(wu), t(wd), k, t(bias)).numpy()
+    out_shared = fused_moe_forward(t(x), t(logits), t(wg), t(wu), t(wd), k, t(bias),
+                                   shared=(t(sg), t(su), t(sd))).numpy()
+    out_shard = fused_moe_forward(t(x), t(logits), t(wg[2:6]), t(wu[2:6]), t(wd[2:6]), k, t(bias),
+                                  expert_range=(2, 4)).numpy()
+    qg, s_g = quantize_rows_fp8(wg)
+    qu, s_u = quantize_rows_fp8(wu)
+    qd, s_d = quantize_rows_fp8(wd)
+    out_fp8 = w8a8_forward(t(x), t(logits), qg, s_g, qu, s_u, qd, s_d, k, t(bias), fmt="fp8").numpy()
+    np.savez_compressed(OUT / "extensions_small.npz", x=x, bias=bias, w_router=wr, w_gate=wg, w_up=wu,
+                        w_down=wd, w_gate_shared=sg, w_up_shared=su, w_down_shared=sd, top_k=np.int32(k),
+                        logits=logits, ids=ids, weights=w, out_router=out_router, out_shared=out_shared,
+                        out_shard=out_shard, q_gate_fp8=qg, s_gate_fp8=s_g, out_fp8=out_fp8)
+
+
 if __name__ == "__main__":
     torch.set_num_threads(1)
     prerouted()
     fused()
+    extensions()
     for f in sorted(OUT.glob("*.npz")):
         print(f.name, f.stat().st_size)

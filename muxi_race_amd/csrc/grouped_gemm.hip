@@ -266,7 +266,17 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < L::WAVES_N; ++j) amax = fmaxf(amax, red[j * BM + mrow]);
-      const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
+      // int8: scale amax/127.  fp8: the power-of-two scale 2^j (amax <= 448 * 2^j),
+      // which Stage 2's f8 MFMA applies itself; dividing by it is exact.
+      float inv, hscale;
+      if constexpr (F8) {
+        const int sb = pow2_scale_e8m0(amax);
+        hscale = amax > 0.0f ? scale_from_e8m0(sb) : 0.0f;
+        inv = amax > 0.0f ? scale_from_e8m0(254 - sb) : 0.0f;  // 2^-j (sb = 0: 2^127, the exact inverse of 2^-127)
+      } else {
+        inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
+        hscale = amax / qmax<F8>();
+      }
       if (mrow < actual) {
         const int64_t grow = row0 + mrow;
         int8_t* hrow = reinterpret_cast<int8_t*>(p.h) + grow * p.h_ld;
@@ -281,7 +291,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
             *reinterpret_cast<uint32_t*>(hrow + n) = packed;
           }
         // scales are stored block-major: [I/128][hs_stride]
-        if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = amax / qmax<F8>();
+        if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = hscale;
       }
     }
   }
@@ -531,19 +541,17 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           }
         } else {
           // One K step of 8-bit operands is one 128-column scale block of the
-          // intermediate: partial product (exact int32 for int8, fp32 for
-          // fp8), then acc += partial * s_h[row, block].
+          // intermediate, with one scale per token row.
           const float* scl = reinterpret_cast<const float*>(st + SCALES);
           float sc[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) sc[b] = scl[xr0 + 32 * b + (l & 31)];
-          using PAcc = typename std::conditional<F8, f32x16, i32x16>::type;
-          PAcc ia[L::NBN][NB];
-#pragma unroll
-          for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) ia[a][b] = PAcc{};
           if constexpr (F8) {
+            // fp8: the row scales are powers of two, applied by the MFMA itself
+            // (E8M0 exponent byte of each token row's scale), straight into acc
+            int sb[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) sb[b] = (int)(__float_as_uint(sc[b]) >> 23);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
               load_frags(0, 2 * j);
@@ -552,9 +560,17 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #pragma unroll
               for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-                for (int b = 0; b < NB; ++b) ia[a][b] = mma8(wf[0][a], wf[1][a], af[0][b], af[1][b], ia[a][b]);
+                for (int b = 0; b < NB; ++b)
+                  acc[a][b] = mma8_scale_b(wf[0][a], wf[1][a], af[0][b], af[1][b], acc[a][b], sb[b]);
             }
           } else {
+            // int8: exact int32 partial product of the step, then
+            // acc += partial * s_h[row, block]
+            i32x16 ia[L::NBN][NB];
+#pragma unroll
+            for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+              for (int b = 0; b < NB; ++b) ia[a][b] = i32x16{};
             load_frags(0, 0);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
@@ -566,13 +582,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
             }
+#pragma unroll
+            for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+              for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
           }
-#pragma unroll
-          for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
         }
       }
     }

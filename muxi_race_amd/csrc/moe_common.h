@@ -190,6 +190,30 @@ __device__ __forceinline__ f32x16 mma8(u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1, f
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// As mma8, with the B operand's rows scaled by 2^(sb - 127) (E8M0 byte sb):
+// lane l gives the scale of B row l % 32 -- lanes l and l + 32 each cover one
+// 32-element K block of that row, and the callers pass the same scale for
+// both, since a row's scale is constant over the 64 K elements.
+__device__ __forceinline__ f32x16 mma8_scale_b(u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1, f32x16 c, int sb) {
+  const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+  const i32x8 b = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
+}
+
+// Power-of-two scale for an fp8 block of maximum |value| amax > 0: 2^j with
+// the smallest j such that amax <= 448 * 2^j (so amax / 2^j lies in (224,
+// 448] and dividing by it is exact), j >= -127.  Returned as its E8M0 byte
+// j + 127; scale_from_e8m0 gives the float (2^-127 as a denormal).
+__device__ __forceinline__ int pow2_scale_e8m0(float amax) {
+  const uint32_t u = __float_as_uint(amax);
+  const int e = (int)((u >> 23) & 0xFF) - 127;                  // amax = m * 2^e, m in [1, 2)
+  int j = e - 8 + ((u & 0x7FFFFFu) > 0x600000u ? 1 : 0);       // 448 = 1.75 * 2^8
+  return j < -127 ? 0 : j + 127;
+}
+__device__ __forceinline__ float scale_from_e8m0(int b) {
+  return b == 0 ? __uint_as_float(0x00400000u) : __uint_as_float((uint32_t)b << 23);
+}
+
 // silu(g) * u = u * g / (1 + 2^(-g*log2e)) in fp32 (v_exp_f32 + v_rcp_f32).
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e));

@@ -28,11 +28,12 @@ Pinning (how each function is checked independently of its own formula):
                            hand-made rows, round-half-away edge cases, and the
                            fp16 oracle within the north-star W8A8 gate
                            (tests/test_oracle_w8a8.py).
-* ``fp8_e4m3_codes`` / ``quantize_rows_fp8`` / ``w8a8_forward(fmt="fp8")`` --
+* ``fp8_e4m3_codes`` / ``quantize_rows_fp8`` / ``pow2_scales`` / ``w8a8_forward(fmt="fp8")`` --
                            torch's own float8_e4m3fn conversion on every code
                            boundary and midpoint (ties to even), hand-made
                            codes, the e4m3 value table against the format's
-                           definition, and the fp16 oracle within the W8A8
+                           definition, power-of-two scales against brute
+                           force over j, and the fp16 oracle within the W8A8
                            gate (tests/test_oracle_fp8.py).
 * ``fused_moe_forward(shared=)`` -- exact doubling closed form and the dense
                            SwiGLU difference (tests/test_oracle_core.py).
@@ -49,6 +50,7 @@ from .moe_ref import (  # noqa: F401
     fused_moe_forward,
     quantize_rows_int8,
     quantize_rows_fp8,
+    pow2_scales,
     fp8_e4m3_codes,
     FP8_E4M3_VALUES,
     w8a8_forward,

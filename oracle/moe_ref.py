@@ -301,13 +301,30 @@ def _fp8_table() -> np.ndarray:
 FP8_E4M3_VALUES = _fp8_table()
 
 
-def quantize_rows_fp8(w):
+def pow2_scales(amax) -> np.ndarray:
+    """Power-of-two fp8 block scales: 2**j with the smallest j >= -127 such
+    that amax <= 448 * 2**j (amax = m * 2**e, m in [1, 2): j = e - 8 + [m >
+    1.75]); 0 where amax == 0.  float32 (2**-127 is a denormal)."""
+    amax = np.asarray(amax, dtype=np.float32)
+    m, e = np.frexp(amax.astype(np.float64))       # amax = m * 2**e, m in [0.5, 1)
+    j = (e - 1) - 8 + (2 * m > 1.75)
+    j = np.maximum(j, -127)
+    return np.where(amax > 0, np.ldexp(1.0, j), 0.0).astype(np.float32)
+
+
+def quantize_rows_fp8(w, pow2: bool = False):
     """Per-row fp8 e4m3: amax = max|w|, scale = amax/448, code =
     e4m3(w * (448/amax)) (product rounded to fp32, then to e4m3 nearest even).
-    Rows with amax == 0 give code 0 and scale 0.  Returns (codes uint8
-    [..., K], scale float32 [...])."""
+    With ``pow2`` the scale is ``pow2_scales(amax)`` and the code e4m3(w /
+    scale), an exact scaling.  Rows with amax == 0 give code 0 and scale 0.
+    Returns (codes uint8 [..., K], scale float32 [...])."""
     a = _as_t(w).float().numpy().astype(np.float32)
     amax = np.abs(a).max(axis=-1).astype(np.float32)
+    if pow2:
+        scale = pow2_scales(amax)
+        with np.errstate(divide="ignore"):
+            inv = np.where(scale > 0, 1.0 / scale.astype(np.float64), 0.0).astype(np.float32)
+        return fp8_e4m3_codes((a * inv[..., None]).astype(np.float32)), scale
     with np.errstate(divide="ignore"):
         inv = np.where(amax > 0, np.float32(448.0) / amax, np.float32(0.0)).astype(np.float32)
     scale = (amax / np.float32(448.0)).astype(np.float32)
@@ -337,7 +354,9 @@ def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k
     s_down[e, n] and the routing weight; pairs are combined in choice order.
     fmt "int8": int8 codes (wq_* int8); "fp8": OCP e4m3 codes (wq_* uint8),
     whose products are exact in float64 (8 significant bits each, sums of at
-    most 2**14 terms between 2**-18 and 2**18); the GPU sums them in fp32.
+    most 2**14 terms between 2**-18 and 2**18); the GPU sums them in fp32.  The
+    fp8 intermediate takes power-of-two scales (``pow2_scales``), which the
+    GPU's f8 MFMA applies itself.
     """
     if fmt == "fp8":
         quant = quantize_rows_fp8
@@ -372,7 +391,7 @@ def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k
         h = silu_mul(torch.from_numpy(g), torch.from_numpy(u)).numpy().astype(np.float32)
         nb = I // scale_block
         hb = h.reshape(n, nb, scale_block)
-        hq, sh = quant(hb)                       # [n, nb, 128], [n, nb]
+        hq, sh = quantize_rows_fp8(hb, pow2=True) if fmt == "fp8" else quant(hb)  # [n, nb, 128], [n, nb]
         hq = val(hq)
         wd = val(wq_down[e])
         acc = np.zeros((n, H), dtype=np.float32)

@@ -84,3 +84,35 @@ def test_fp8_forward_against_fp16_oracle():
     out = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k, fmt="fp8").float()
     rel = float((out - ref).norm() / ref.norm())
     assert 5e-3 < rel < FP8_REL_L2, rel
+
+
+def test_pow2_scales_brute_force():
+    """pow2_scales(amax) is the smallest 2**j (j >= -127) with amax <= 448 * 2**j,
+    checked by trying every j, on random magnitudes and the edges amax = 448 * 2**j
+    (and the floats beside it)."""
+    from oracle import pow2_scales
+    rng = np.random.default_rng(7)
+    a = (10.0 ** rng.uniform(-40, 30, 3000)).astype(np.float32)
+    edges = np.float32([448.0 * 2.0 ** j for j in (-20, -1, 0, 3)])
+    a = np.concatenate([a, edges, np.nextafter(edges, np.float32(np.inf)), np.nextafter(edges, np.float32(0))])
+    a = np.concatenate([a, np.float32([0.0, 1e-45, 2.0 ** -130])])
+    s = pow2_scales(a)
+    for amax, sc in zip(a.astype(np.float64), s.astype(np.float64)):
+        if amax == 0:
+            assert sc == 0
+            continue
+        js = [j for j in range(-127, 128) if amax <= 448.0 * 2.0 ** j]
+        assert sc == 2.0 ** js[0], (amax, sc)
+    ok = (a > 2.0 ** -100)
+    assert ((a[ok] / s[ok] > 224) & (a[ok] / s[ok] <= 448)).all()
+
+
+def test_pow2_fp8_rows_are_exact_scalings():
+    from oracle import quantize_rows_fp8
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((50, 128)) * 10.0 ** rng.uniform(-3, 3, (50, 1))).astype(np.float32)
+    q, s = quantize_rows_fp8(w, pow2=True)
+    assert (np.log2(s) == np.round(np.log2(s))).all()
+    # the codes are those of w / s (exact division by a power of two)
+    np.testing.assert_array_equal(q, fp8_e4m3_codes((w / s[:, None]).astype(np.float32)))
+    assert (np.abs(FP8_E4M3_VALUES[q]).max(axis=1) >= 224).all()  # (224, 448] before rounding

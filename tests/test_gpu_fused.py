@@ -129,3 +129,10 @@ def test_empty_batch():
     out, (ids, w) = fused_moe(x, inp["logits"][:0], inp["wg"], inp["wu"], inp["wd"], 2, return_routing=True)
     torch.cuda.synchronize()
     assert out.shape == (0, 128) and ids.shape == (0, 2) and w.shape == (0, 2)
+
+
+def test_large_batch_sampled():
+    """A large prefill batch: dsv3 shape at T = 32768 (262144 routed pairs, the
+    64-workgroup align, 3.8 GB of per-pair rows), checked on sampled tokens."""
+    inp = moe_inputs("dsv3", 12, T=32768)
+    _check(inp, sample=6, what="dsv3 T=32768")

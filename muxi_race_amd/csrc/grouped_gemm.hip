@@ -485,6 +485,40 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   const int live = (actual - wm * L::WTM + 31) / 32;  // see Stage 1
   const int xr0 = wm * L::WTM;       // stage row of this wave's first token row
   const int wr0 = rx + wn * L::WTN;  // ... of its first weight row
+
+  // Output row and routing weight of each of this lane's token rows, loaded
+  // before the K loop so that their latency hides behind it.
+  // (Loads are unconditional, all rows' ids first: row0 + m lies inside the
+  // item's rows of the sorted buffer; padding rows take pair 0's weight and
+  // are never stored.)
+  int64_t orow[L::NBM];
+  float wr[L::NBM];
+  if constexpr (FUSED) {
+    int pid[L::NBM];
+#pragma unroll
+    for (int b = 0; b < L::NBM; ++b) pid[b] = p.sorted_ids[row0 + xr0 + 32 * b + (l & 31)];
+#pragma unroll
+    for (int b = 0; b < L::NBM; ++b) {
+      const bool valid = xr0 + 32 * b + (l & 31) < actual;
+      orow[b] = valid ? pid[b] : 0;
+      wr[b] = reinterpret_cast<const float*>(p.routed)[valid ? pid[b] : 0];
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < L::NBM; ++b) {
+      const int m = xr0 + 32 * b + (l & 31);
+      orow[b] = row0 + m;
+      // raw-order index (problem_detail.json:50 note 2), clamped to the
+      // buffer as submission.py:1286-1288 does
+      int64_t ridx = (int64_t)go_e + (row0 - gpo_e) + m;
+      ridx = ridx >= p.V ? p.V - 1 : ridx;
+      ridx = ridx < 0 ? 0 : ridx;
+      wr[b] = 0.0f;
+      if (m < actual && p.V > 0)
+        wr[b] = p.routed_f16 ? (float)reinterpret_cast<const _Float16*>(p.routed)[ridx]
+                             : reinterpret_cast<const float*>(p.routed)[ridx];
+    }
+  }
   f32x16 acc[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -600,24 +634,6 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   for (int b = 0; b < L::NBM; ++b) {
     const int m = xr0 + 32 * b + (l & 31);
     const bool valid = m < actual;
-    float wr = 0.0f;
-    int64_t orow = row0 + m;
-    if (valid) {
-      if (FUSED) {
-        const int pid = p.sorted_ids[row0 + m];
-        wr = reinterpret_cast<const float*>(p.routed)[pid];
-        orow = pid;
-      } else {
-        // raw-order index (problem_detail.json:50 note 2), clamped to the
-        // buffer as submission.py:1286-1288 does
-        int64_t ridx = (int64_t)go_e + (row0 - gpo_e) + m;
-        ridx = ridx >= p.V ? p.V - 1 : ridx;
-        ridx = ridx < 0 ? 0 : ridx;
-        if (p.V > 0)
-          wr = p.routed_f16 ? (float)reinterpret_cast<const _Float16*>(p.routed)[ridx]
-                            : reinterpret_cast<const float*>(p.routed)[ridx];
-      }
-    }
     if (FUSED && !valid) continue;
 #pragma unroll
     for (int a = 0; a < L::NBN; ++a)
@@ -632,9 +648,9 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           float y = acc[a][b][4 * rg + q];
           if constexpr (I8) y = y * sd[q];
           // select, never multiply, so NaN/Inf garbage in padding rows cannot leak
-          v[q] = valid ? (_Float16)(y * wr) : (_Float16)0.0f;
+          v[q] = valid ? (_Float16)(y * wr[b]) : (_Float16)0.0f;
         }
-        *reinterpret_cast<f16x4*>(o + orow * p.H + n) = v;
+        *reinterpret_cast<f16x4*>(o + orow[b] * p.H + n) = v;
       }
   }
 }

@@ -127,6 +127,33 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   const int xr0 = wm * L::WTM;           // stage row of this wave's first token row
   const int gr0 = rx + wn * L::WTN;      // ... of its first gate row
   const int ur0 = rx + rw + wn * L::WTN; // ... of its first up row
+
+  // 8-bit: the dequantisation scales of this lane's token rows and output
+  // features, loaded before the K loop so that their latency hides behind it
+  // (padding rows read token 0's scale and are never stored).
+  float sxv[L::NBM];
+  f32x4 sgv[L::NBN][4], suv[L::NBN][4];
+  if constexpr (I8) {
+    const int lq = lane_id();
+    int pid[L::NBM];
+#pragma unroll
+    for (int b = 0; b < L::NBM; ++b) pid[b] = p.sorted_ids[row0 + xr0 + 32 * b + (lq & 31)];
+#pragma unroll
+    for (int b = 0; b < L::NBM; ++b) {
+      const bool valid = xr0 + 32 * b + (lq & 31) < actual;
+      sxv[b] = p.x_scale[valid ? pid[b] / p.topk : 0];
+    }
+    const float* sgrow = p.sg + (int64_t)e * p.I;
+    const float* surow = p.su + (int64_t)e * p.I;
+#pragma unroll
+    for (int a = 0; a < L::NBN; ++a)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (lq >> 5);
+        sgv[a][rg] = *reinterpret_cast<const f32x4*>(sgrow + n);
+        suv[a][rg] = *reinterpret_cast<const f32x4*>(surow + n);
+      }
+  }
   Acc ag[L::NBN][L::NBM], au[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
@@ -232,25 +259,19 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     // and the WAVES_N waves.
     float* red = reinterpret_cast<float*>(smem);  // [WAVES_N][BM]; loop ended with a barrier
     float hv[L::NBM][L::NBN][16];
-    const float* sgrow = p.sg + (int64_t)e * p.I;
-    const float* surow = p.su + (int64_t)e * p.I;
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
       const int m = xr0 + 32 * b + (l & 31);
-      float sx = 0.0f;
-      if (m < actual) sx = p.x_scale[p.sorted_ids[row0 + m] / p.topk];
+      const float sx = m < actual ? sxv[b] : 0.0f;
       float amax = 0.0f;
 #pragma unroll
       for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
-          const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
-          const f32x4 sgv = *reinterpret_cast<const f32x4*>(sgrow + n);
-          const f32x4 suv = *reinterpret_cast<const f32x4*>(surow + n);
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float g = ((float)ag[a][b][4 * rg + q] * sx) * sgv[q];
-            const float u = ((float)au[a][b][4 * rg + q] * sx) * suv[q];
+            const float g = ((float)ag[a][b][4 * rg + q] * sx) * sgv[a][rg][q];
+            const float u = ((float)au[a][b][4 * rg + q] * sx) * suv[a][rg][q];
             const float h = silu_mul(g, u);
             hv[b][a][4 * rg + q] = h;
             amax = fmaxf(amax, fabsf(h));

@@ -199,8 +199,8 @@ def main():
     w8 = (args.config == "w8a8" or args.w8a8 or args.fp8) and not args.fp16
     fmt = "fp8" if args.fp8 else "int8"
     L = lib()
-    bm = args.block_m or int(L.moe_pick_block_m(T, E, k))
-    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, int(w8))
+    bm = args.block_m  # 0: the library picks (reported below as its 128/64/32 choice)
+    nbytes = L.moe_fused_workspace_bytes(T, H, I, E, k, bm, (2 if fmt == "fp8" else 1) if w8 else 0)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     out = torch.full((T, H), float("nan"), dtype=torch.float16, device=dev)  # poisoned: the step must write it all
     ids = torch.empty((T, k), dtype=torch.int32, device=dev)
@@ -365,7 +365,7 @@ def main():
         gs_ = torch.Generator(device=dev).manual_seed(SEED + 3)
         sw = [torch.randn(shape, generator=gs_, device=dev, dtype=torch.float16) * 0.02
               for shape in ((I, H), (I, H), (H, I))]
-        sbm = args.block_m or int(L.moe_pick_block_m(T, E + 1, k + 1))
+        sbm = args.block_m
         sws = torch.empty(int(L.moe_fused_shared_workspace_bytes(T, H, I, E, k, sbm)), dtype=torch.uint8, device=dev)
         sout = torch.empty_like(out)
         sargs = head[:2] + [P(0), head[2]] + [P(inp[n].data_ptr()) for n in ("wg", "wu", "wd")] + \
@@ -375,7 +375,7 @@ def main():
         b_ms = timed(fwd, cargs, name)  # routed-only step, timed the same way beside it
         s_bytes = op_bytes + 3.0 * H * I * 2
         s_flops = flops + 6.0 * H * I * T
-        shared = {"shared_ms": round(s_ms, 4), "routed_only_ms": round(b_ms, 4), "block_m": sbm,
+        shared = {"shared_ms": round(s_ms, 4), "routed_only_ms": round(b_ms, 4), "block_m": sbm or int(L.moe_pick_block_m(T, E + 1, k + 1)),
                   "extra_ms": round(s_ms - b_ms, 4),
                   "gb_per_s": round(s_bytes / (s_ms * 1e-3) / 1e9, 1),
                   "tflops": round(s_flops / (s_ms * 1e-3) / 1e12, 2),
@@ -423,7 +423,7 @@ def main():
         if E % G:
             raise SystemExit(f"--ep-shards {G} must divide E={E}")
         n = E // G
-        sbm = args.block_m or int(L.moe_pick_block_m(T, E, k))
+        sbm = args.block_m
         ews = torch.empty(int(L.moe_fused_shard_workspace_bytes(T, H, I, E, k, n, sbm)), dtype=torch.uint8,
                           device=dev)
         eout = torch.empty_like(out)
@@ -477,7 +477,7 @@ def main():
         "config": {"workload": f"fused MoE {args.config}: T={T} H={H} I={I} E={E} top{k} "
                                + (f"W8A8 {fmt}" if w8 else "fp16"),
                    "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
-                   "block_m": bm, "experts_touched": int(touched),
+                   "block_m": bm or int(L.moe_pick_block_m(T, E, k)), "experts_touched": int(touched),
                    "weight_layout": f"{fmt} dense" if w8 else args.weights},
         "gb_per_s": round(gbs, 1),
         "frac_mfma_peak": round(tflops / peak_c, 4),

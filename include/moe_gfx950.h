@@ -122,8 +122,10 @@ int moe_align(const int32_t* topk_ids, int64_t T, int64_t k, int64_t E, int64_t 
  * SiLU*up) -> Stage2 (down GEMM * routing weight) -> k-way combine into token
  * order.  x fp16 [T, H]; logits fp32 [T, E]; bias fp32 [E] or NULL; weights as
  * for moe_run_prerouted; out fp16 [T, H].  block_m in {32, 64, 128} or 0 for
- * the library's choice.  topk_ids_out / topk_weights_out ([T, k]) may be NULL;
- * when given they receive the routing result.
+ * the library's choice (which may pad experts to 256 rows and run one stage
+ * on 256-row items).  topk_ids_out / topk_weights_out ([T, k]) may be NULL;
+ * when given they receive the routing result.  moe_fused_workspace_bytes:
+ * w8a8 = 0 for fp16, 1 for int8, 2 for fp8.
  * ---------------------------------------------------------------------- */
 int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                   int64_t block_m, int w8a8);
@@ -260,7 +262,8 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
  * zero rows give code 0 and scale 0.  Activations are quantised per token and
  * the SiLU*up intermediate per (row, 128 columns) the same way, inside the call.
  * moe_fused_forward_fp8 takes stage_events as moe_fused_forward_events (or
- * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 1).  Extends the
+ * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 2) (one sized with
+ * w8a8 = 1 also works, without the 256-row padding).  Extends the
  * reference's W8A8 variant (submission_v321_int8_fixed.py:421-506) to the fp8
  * MFMA of this part; the reference has no fp8 path.
  * ---------------------------------------------------------------------- */

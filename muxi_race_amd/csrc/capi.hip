@@ -67,6 +67,22 @@ int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
   return 128;
 }
 
+// Rows per block of the align padding.  block_m != 0 is the caller's choice,
+// used by both stages.  0: pick_bm's size, except that 128 becomes 256 where a
+// 256-row item is faster for one stage and H is a multiple of 256 (measured):
+// Stage 1 of fp16 with >= 384 routed rows per expert on average (mixtral-like),
+// Stage 2 of fp8 with >= 192.  The other stage keeps 128-row items; those in
+// a block's empty second half end at once.  int8 keeps 128.
+int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int qt, int64_t block_m) {
+  if (block_m) return block_m;
+  const int64_t bm = pick_bm(T, E, k);
+  if (bm != 128 || H % 256) return bm;
+  const int64_t avg = (T * k + E - 1) / E;
+  if (qt == moe::kQF16) return avg >= 384 ? 256 : 128;
+  if (qt == moe::kQF8) return avg >= 192 ? 256 : 128;
+  return 128;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_dims(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm) {
@@ -74,7 +90,7 @@ int check_dims(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm
   if (k > E || k > 32) return fail(MOE_ERR_UNSUPPORTED, "top_k=%lld must be <= min(E, 32)", (long long)k);
   if (E > 1024) return fail(MOE_ERR_UNSUPPORTED, "E=%lld > 1024", (long long)E);
   if (H <= 0 || I <= 0 || H % 128 || I % 128) return fail(MOE_ERR_UNSUPPORTED, "H=%lld and I=%lld must be positive multiples of 128", (long long)H, (long long)I);
-  if (bm != 32 && bm != 64 && bm != 128) return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {32,64,128}", (long long)bm);
+  if (bm != 32 && bm != 64 && bm != 128 && bm != 256) return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {32,64,128}", (long long)bm);
   if (cap_rows(T, k, E, bm) * I >= ((int64_t)1 << 31) * 2 || T * k >= ((int64_t)1 << 31)) return fail(MOE_ERR_UNSUPPORTED, "problem too large for 32-bit row indices");
   return MOE_OK;
 }
@@ -212,7 +228,8 @@ int64_t moe_pick_block_m(int64_t T, int64_t E, int64_t k) { return pick_bm(T, E,
 int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                   int64_t block_m, int w8a8) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  if (block_m == 0) block_m = pick_bm(T, E, k);
+  // w8a8: 0 fp16, 1 int8, 2 fp8
+  block_m = align_bm(T, E, k, H, w8a8 == 0 ? moe::kQF16 : (w8a8 == 2 ? moe::kQF8 : moe::kQI8), block_m);
   return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
 }
 
@@ -239,7 +256,9 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   if (shared && (w8 || !wg_s || !wu_s || !wd_s))
     return fail(w8 ? MOE_ERR_UNSUPPORTED : MOE_ERR_INVALID_ARG, w8 ? "the shared expert is supported on the fp16 path" : "null pointer argument");
   const int64_t Ee = E + (shared ? 1 : 0), ke = k + (shared ? 1 : 0);  // experts / choices incl. the shared one
-  if (block_m == 0) block_m = pick_bm(T, shard ? E_route : Ee, ke);
+  if (block_m != 0 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {0,32,64,128}", (long long)block_m);
+  block_m = align_bm(T, shard ? E_route : Ee, ke, H, qt, block_m);
   int rc = check_dims(T, H, I, shard ? E_route : Ee, ke, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
@@ -260,9 +279,16 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(workspace) || (w8 && (!aligned16(sg) || !aligned16(su) || !aligned16(sd))) ||
       (shared && (!aligned16(wg_s) || !aligned16(wu_s) || !aligned16(wd_s))))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
+  const int64_t router_ws = w_router ? moe_router_workspace_bytes(T, H, E) : 0;
+  // a workspace sized for the 128-row padding (fp8 sized as int8) keeps it
+  if (block_m == 256 && workspace_bytes < fused_layout(T, H, I, Ee, ke, 256, w8).total + router_ws) block_m = 128;
   const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, w8);
-  const int64_t need = L.total + (w_router ? moe_router_workspace_bytes(T, H, E) : 0);
+  const int64_t need = L.total + router_ws;
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
+  // rows per item of each stage: block_m, except over the 256-row padding,
+  // where one stage takes 256-row items (see align_bm)
+  const int64_t bm1 = block_m == 256 && qt == moe::kQF16 ? 256 : (block_m == 256 ? 128 : block_m);
+  const int64_t bm2 = block_m == 256 && qt == moe::kQF8 ? 256 : (block_m == 256 ? 128 : block_m);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);
@@ -311,7 +337,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p1.E = (int)Ee;
   p1.H = H;
   p1.I = I;
-  if ((rc = check_launch(moe::launch_stage1(p1, (int)block_m, qt, true, rows / block_m, s), "stage1"))) return rc;
+  if ((rc = check_launch(moe::launch_stage1(p1, (int)bm1, qt, true, rows / bm1, s), "stage1"))) return rc;
   mark(4);
 
   moe::Stage2Params p2{};
@@ -334,7 +360,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.E = (int)Ee;
   p2.H = H;
   p2.I = I;
-  if ((rc = check_launch(moe::launch_stage2(p2, (int)block_m, qt, true, rows / block_m, s), "stage2"))) return rc;
+  if ((rc = check_launch(moe::launch_stage2(p2, (int)bm2, qt, true, rows / bm2, s), "stage2"))) return rc;
   mark(5);
   rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s, shard ? ids : nullptr, (int)e_begin, (int)E),
                     "combine");
@@ -372,7 +398,7 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
 int64_t moe_fused_shared_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                          int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  if (block_m == 0) block_m = pick_bm(T, E + 1, k + 1);
+  block_m = align_bm(T, E + 1, k + 1, H, moe::kQF16, block_m);
   return fused_layout(T, H, I, E + 1, k + 1, block_m, false).total + moe_router_workspace_bytes(T, H, E);
 }
 
@@ -393,7 +419,7 @@ int64_t moe_fused_ex_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                      int shared, int with_router) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   const int64_t s = shared ? 1 : 0;
-  if (block_m == 0) block_m = pick_bm(T, E + s, k + s);
+  block_m = align_bm(T, E + s, k + s, H, moe::kQF16, block_m);
   return fused_layout(T, H, I, E + s, k + s, block_m, false).total + (with_router ? moe_router_workspace_bytes(T, H, E) : 0);
 }
 
@@ -414,7 +440,7 @@ int moe_fused_forward_ex(const void* x, const float* logits, const void* w_route
 int64_t moe_fused_shard_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
                                         int64_t E_local, int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E_total <= 0 || E_local <= 0 || k <= 0) return 0;
-  if (block_m == 0) block_m = pick_bm(T, E_total, k);
+  block_m = align_bm(T, E_total, k, H, moe::kQF16, block_m);
   return fused_layout(T, H, I, E_local, k, block_m, false).total;
 }
 

@@ -702,10 +702,10 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #define MOE_S2_STAGES_32 4
 #endif
 constexpr int s1_stages(int bm) {
-  return bm == 128 ? MOE_S1_STAGES_128 : (bm == 64 ? MOE_S1_STAGES_64 : MOE_S1_STAGES_32);
+  return bm == 256 ? 2 : bm == 128 ? MOE_S1_STAGES_128 : (bm == 64 ? MOE_S1_STAGES_64 : MOE_S1_STAGES_32);
 }
 constexpr int s2_stages(int bm) {
-  return bm == 128 ? MOE_S2_STAGES_128 : (bm == 64 ? MOE_S2_STAGES_64 : MOE_S2_STAGES_32);
+  return bm == 256 ? 2 : bm == 128 ? MOE_S2_STAGES_128 : (bm == 64 ? MOE_S2_STAGES_64 : MOE_S2_STAGES_32);
 }
 
 // Waves per workgroup of the 128-row tiles (4 = one wave per SIMD; 8 = two,
@@ -793,6 +793,10 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, int qt, bool g
       if (qt == kQI8) return go1<128, 2, NW, kQI8, true, false>(p, grid, s);
       if (qt == kQF8) return go1<128, 2, NW, kQF8, true, false>(p, grid, s);
       return go1<128, 2, NW, kQF16, true, kPair>(p, grid, s);
+    case 256:
+      // fp16, 256 token rows x (128 gate + 128 up) rows: two 64 KiB stages
+      if (qt == kQF16) return go1<256, 4, 8, kQF16, true, false>(p, grid, s);
+      return hipErrorInvalidValue;
   }
   return hipErrorInvalidValue;
 }
@@ -822,6 +826,10 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, int qt, bool f
       if (qt == kQI8) return go2_128<kQI8, true>(p, mb, s);
       if (qt == kQF8) return go2_128<kQF8, true>(p, mb, s);
       return go2_128<kQF16, true>(p, mb, s);
+    case 256:
+      // fp8, 256 token rows x 256 weight rows: two 64 KiB stages
+      if (qt == kQF8 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQF8, true, false>(p, mb, s);
+      return hipErrorInvalidValue;
   }
   return hipErrorInvalidValue;
 }

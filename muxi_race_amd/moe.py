@@ -211,7 +211,9 @@ def pick_block_m(T: int, E: int, top_k: int) -> int:
 
 
 def fused_workspace_bytes(T, H, I, E, top_k, block_m=0, w8a8=False) -> int:
-    return int(lib().moe_fused_workspace_bytes(T, H, I, E, top_k, block_m, int(bool(w8a8))))
+    """Workspace of fused_moe; w8a8: False (fp16), True / "int8", or "fp8"."""
+    flag = 0 if not w8a8 else (2 if w8a8 == "fp8" else 1)
+    return int(lib().moe_fused_workspace_bytes(T, H, I, E, top_k, block_m, flag))
 
 
 # ---------------------------------------------------------------------------
@@ -358,7 +360,7 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
     if expert_range is not None:
         if not (w_gate.is_contiguous() and w_up.is_contiguous() and w_down.is_contiguous()):
             raise ValueError("expert_range takes dense weights")
-        bm = block_m or int(L.moe_pick_block_m(T, E_route, top_k))
+        bm = block_m  # 0: the library picks
         ws = _workspace(dev, ("fused", False), L.moe_fused_shard_workspace_bytes(T, H, I, E_route, top_k, E, bm))
         ids = torch.empty((T, top_k), dtype=torch.int32, device=dev) if return_routing else None
         wts = torch.empty((T, top_k), dtype=torch.float32, device=dev) if return_routing else None
@@ -369,14 +371,14 @@ def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
         check(rc, "fused_moe")
         return (out, (ids, wts)) if return_routing else out
     ncol = top_k + (shared_expert is not None)
-    bm = block_m or int(L.moe_pick_block_m(T, E + (shared_expert is not None), ncol))
+    bm = block_m  # 0: the library picks the block rows (and a 256-row padding where that is faster)
     if shared_expert is not None:
         nbytes = L.moe_fused_shared_workspace_bytes(T, H, I, E, top_k, bm)
     elif router_weight is not None:
         nbytes = L.moe_fused_hidden_workspace_bytes(T, H, I, E, top_k, bm)
     else:
-        nbytes = L.moe_fused_workspace_bytes(T, H, I, E, top_k, bm, int(w8a8 is not None))
-    ws = _workspace(dev, ("fused", w8a8 is not None), nbytes)
+        nbytes = L.moe_fused_workspace_bytes(T, H, I, E, top_k, bm, 0 if w8a8 is None else (2 if w8a8.fmt == "fp8" else 1))
+    ws = _workspace(dev, ("fused", None if w8a8 is None else w8a8.fmt), nbytes)
     ids = torch.empty((T, ncol), dtype=torch.int32, device=dev) if return_routing else None
     wts = torch.empty((T, ncol), dtype=torch.float32, device=dev) if return_routing else None
     strided = w8a8 is None and not (w_gate.is_contiguous() and w_up.is_contiguous() and w_down.is_contiguous())

@@ -109,3 +109,17 @@ def moe_inputs(name, seed, device="cuda", T=None):
     wu = mk((E, I, H))
     wd = mk((E, H, I))
     return dict(x=x, logits=logits, bias=bias, wg=wg, wu=wu, wd=wd, k=k, T=T, H=H, I=I, E=E)
+
+
+def skewed_8bit_case(seed, device="cuda"):
+    """T=800, H=512 (a multiple of 256), 200 routed rows per expert: 128-row
+    blocks picked, and the fp8 path pads experts to 256 rows.  Biases give an
+    empty expert, experts of <= 128 rows (an empty second half) and
+    multi-block experts."""
+    g = torch.Generator().manual_seed(seed)
+    T, H, I, E, k = 800, 512, 256, 8, 2
+    return dict(x=torch.randn(T, H, generator=g).half().to(device), logits=torch.randn(T, E, generator=g).to(device),
+                bias=torch.tensor([2.0, 1.5, 1.0, 0.0, -0.5, -1.0, -1.5, -40.0]).to(device),
+                wg=(torch.randn(E, I, H, generator=g) * 0.05).half().to(device),
+                wu=(torch.randn(E, I, H, generator=g) * 0.05).half().to(device),
+                wd=(torch.randn(E, H, I, generator=g) * 0.05).half().to(device), k=k, T=T, H=H, I=I, E=E)

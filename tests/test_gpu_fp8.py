@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import moe_inputs
+from _cases import moe_inputs, skewed_8bit_case
 from conftest import assert_close
 from oracle import fused_moe_forward, quantize_rows_fp8, w8a8_forward
 
@@ -74,6 +74,47 @@ def _run(inp, sample=None, block_m=0, elementwise=False):
 @pytest.mark.parametrize("bm", [0, 32, 64, 128])
 def test_fp8_small(bm):
     _run(moe_inputs("small", 71), block_m=bm, elementwise=True)
+
+
+def test_fp8_256_row_padding_ragged():
+    """fp8 Stage 2 runs 256-row items over the 256-row padding, Stage 1 128-row
+    items.  At T = 800 a few e4m3 boundary flips occur, so the oracle gates are
+    those of the large configs; against explicit 128-row blocks (same
+    intermediate codes, same K order per element) the output must agree."""
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    inp = skewed_8bit_case(76)
+    _run(inp)
+    qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt="fp8")
+    a = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw)
+    b = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw,
+                  block_m=128)
+    torch.cuda.synchronize()
+    assert_close(a, b, atol=1e-3, rtol=1e-3, what="256-row padding vs 128-row blocks")
+
+
+def test_fp8_workspace_sized_as_int8_keeps_128_row_padding():
+    """A caller that sizes the fp8 workspace as int8's (w8a8 = 1) still gets a
+    correct result: the call falls back to the 128-row padding."""
+    import ctypes
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    from muxi_race_amd._lib import lib
+    L = lib()
+    inp = skewed_8bit_case(78)
+    T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
+    qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt="fp8")
+    a = fused_moe(inp["x"], inp["logits"], None, None, None, k, expert_bias=inp["bias"], w8a8=qw)
+    small, full = L.moe_fused_workspace_bytes(T, H, I, E, k, 0, 1), L.moe_fused_workspace_bytes(T, H, I, E, k, 0, 2)
+    assert small < full
+    ws = torch.empty(small, dtype=torch.uint8, device="cuda")
+    b = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    rc = L.moe_fused_forward_fp8(P(inp["x"]), P(inp["logits"]), P(inp["bias"]), P(qw.q_gate), P(qw.s_gate),
+                                 P(qw.q_up), P(qw.s_up), P(qw.q_down), P(qw.s_down), P(b), T, H, I, E, k, 0,
+                                 P(ws), ws.numel(), P(None), P(None),
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), P(None))
+    assert rc == 0, L.moe_last_error_string()
+    torch.cuda.synchronize()
+    assert_close(b, a, atol=1e-3, rtol=1e-3, what="128-row padding vs 256")
 
 
 def test_fp8_w8a8_config_sampled():

@@ -122,6 +122,18 @@ def test_extreme_shapes(T, H, I, E, k):
     _check(_random_case(T, H, I, E, k, T + E), what=f"T={T} H={H} I={I} E={E} k={k}")
 
 
+def test_256_row_padding_ragged():
+    """fp16 experts with >= 384 routed rows on average and H a multiple of 256:
+    align pads experts to 256 rows, Stage 1 runs 256-row items, Stage 2
+    128-row (paired) items.  Skewed biases give full, partial and empty
+    256-row blocks, 128-row halves with no rows, and two empty experts."""
+    inp = _random_case(1536, 512, 384, 8, 2, 77, bias=False)
+    inp["bias"] = torch.tensor([2.5, 2.0, 1.0, 0.5, 0.0, -0.5, -40.0, -40.0], device="cuda")
+    from muxi_race_amd import pick_block_m
+    assert pick_block_m(1536, 8, 2) == 128
+    _check(inp, what="fp16, 256-row padding")
+
+
 def test_empty_batch():
     from muxi_race_amd import fused_moe
     inp = _random_case(1, 128, 128, 4, 2, 5)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import moe_inputs
+from _cases import moe_inputs, skewed_8bit_case
 from conftest import assert_close
 from oracle import fused_moe_forward, quantize_rows_int8, w8a8_forward
 
@@ -55,6 +55,12 @@ def _run(inp, sample=None, block_m=0):
 @pytest.mark.parametrize("bm", [0, 32, 128])
 def test_w8a8_small(bm):
     _run(moe_inputs("small", 21), block_m=bm)
+
+
+def test_w8a8_skewed_ragged():
+    """int8 on the skewed 8-bit case (where fp8 pads experts to 256 rows, int8
+    keeps 128): an empty expert, partial and multi-block experts."""
+    _run(skewed_8bit_case(22))
 
 
 def test_w8a8_config_sampled():

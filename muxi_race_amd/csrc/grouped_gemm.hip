@@ -492,11 +492,14 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // apart (the shared expert's own tensor, same row stride); intermediate rows
   // a_ld bytes apart
   const char* dexp = p.e_shared >= 0 && e == p.e_shared ? p.wd_shared : p.wd + (int64_t)e * p.wd_es;
+  // Token rows past the expert's count (never written by Stage 1) read the
+  // item's first row instead: a cache hit rather than an HBM fetch.  Their
+  // results are never stored.
   LD ld;
 #pragma unroll
   for (int i = 0; i < LD::NI; ++i) {
     const int r = LD::row_of(i);
-    ld.set(i, r < rx ? p.a + (int64_t)(row0 + r) * p.a_ld : dexp + (int64_t)(n0 + r - rx) * p.wd_ld);
+    ld.set(i, r < rx ? p.a + (int64_t)(row0 + (r < actual ? r : 0)) * p.a_ld : dexp + (int64_t)(n0 + r - rx) * p.wd_ld);
   }
 
   const int wave = threadIdx.x >> 6;
@@ -552,7 +555,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   const float* scale_src = nullptr;
   if constexpr (I8) {
     const int r = 64 * wave_id() + l;
-    scale_src = p.a_scale + row0 + (r < rx ? r : 0);
+    scale_src = p.a_scale + row0 + (r < actual ? r : 0);
   }
   constexpr int Q = LD::NI + (I8 ? 1 : 0);
   auto issue = [&](int buf, int k) {

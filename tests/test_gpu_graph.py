@@ -6,7 +6,7 @@ bitwise."""
 import pytest
 import torch
 
-from _cases import moe_inputs
+from _cases import moe_inputs, skewed_8bit_case
 
 pytestmark = pytest.mark.gpu
 
@@ -38,6 +38,20 @@ def test_fp16_forward_replays(name):
     inp = moe_inputs(name, 101)
     _replays_match(lambda: fused_moe(inp["x"], inp["logits"], inp["wg"], inp["wu"], inp["wd"], inp["k"],
                                      expert_bias=inp["bias"]))
+
+
+def test_256_row_padding_replays():
+    """fp16 Stage 1 and fp8 Stage 2 on 256-row items (the 256-row padding)."""
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    g = torch.Generator().manual_seed(104)
+    T, H, I, E, k = 1536, 512, 384, 8, 2  # 384 routed rows per expert
+    x, lg = torch.randn(T, H, generator=g).half().cuda(), torch.randn(T, E, generator=g).cuda()
+    w = [(torch.randn(shape, generator=g) * 0.05).half().cuda() for shape in ((E, I, H), (E, I, H), (E, H, I))]
+    _replays_match(lambda: fused_moe(x, lg, *w, k))
+    inp = skewed_8bit_case(105)
+    qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt="fp8")
+    _replays_match(lambda: fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"],
+                                     expert_bias=inp["bias"], w8a8=qw))
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])

@@ -18,10 +18,12 @@ def _shard(inp, b, n, **kw):
                      inp["k"], expert_bias=inp["bias"], expert_range=(b, n), return_routing=True, **kw)
 
 
-@pytest.mark.parametrize("name,G", [("small", 2), ("small", 8), ("decode", 8), ("dsv3", 8)])
+@pytest.mark.parametrize("name,G", [("small", 2), ("small", 8), ("decode", 8), ("dsv3", 8), ("mixtral", 4)])
 def test_shards_sum_to_full_and_match_oracle(name, G):
     from muxi_race_amd import fused_moe
-    inp = moe_inputs(name, 91, T=1024 if name == "dsv3" else None)
+    # mixtral at T=1536: 384 routed rows per expert over the whole layer, so every
+    # shard runs on the 256-row padding
+    inp = moe_inputs(name, 91, T={"dsv3": 1024, "mixtral": 1536}.get(name))
     E, T = inp["E"], inp["T"]
     full, (fids, fw) = fused_moe(inp["x"], inp["logits"], inp["wg"], inp["wu"], inp["wd"], inp["k"],
                                  expert_bias=inp["bias"], return_routing=True)

@@ -35,9 +35,11 @@ def _run(inp, wg, wu, wd, **kw):
 
 
 @pytest.mark.parametrize("name,bm", [("small", 0), ("small", 32), ("small", 64), ("small", 128), ("decode", 0),
-                                     ("mixtral", 0)])
+                                     ("mixtral", 0), ("mixtral-1536", 0)])
 def test_strided_is_bitwise_dense(name, bm):
-    inp = moe_inputs(name, 61, T=256 if name == "mixtral" else None)
+    # mixtral-1536: 384 routed rows per expert, so the 256-row padding and 256-row Stage 1 items
+    T = {"mixtral": 256, "mixtral-1536": 1536}.get(name)
+    inp = moe_inputs(name.split("-")[0], 61, T=T)
     ref = _run(inp, inp["wg"], inp["wu"], inp["wd"], block_m=bm)
     # gate / up as the halves of one [E, 2I, H] tensor (expert stride 2*I*H)
     w13 = torch.cat([inp["wg"], inp["wu"]], dim=1)

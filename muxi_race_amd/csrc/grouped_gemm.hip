@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
         const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;
         src_row = pid / p.topk;
       } else {
-        src_row = row0 + r;
+        src_row = row0 + (r < actual ? r : 0);  // padding rows: the item's first row, a cache hit
       }
       src = p.x + src_row * kbytes;
     } else if (r < rx + rw) {

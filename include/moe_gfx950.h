@@ -262,8 +262,8 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
  * zero rows give code 0 and scale 0.  Activations are quantised per token and
  * the SiLU*up intermediate per (row, 128 columns) the same way, inside the call.
  * moe_fused_forward_fp8 takes stage_events as moe_fused_forward_events (or
- * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 2) (one sized with
- * w8a8 = 1 also works, without the 256-row padding).  Extends the
+ * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 2) (one sized for
+ * block_m = 128 also works, without the 256-row padding).  Extends the
  * reference's W8A8 variant (submission_v321_int8_fixed.py:421-506) to the fp8
  * MFMA of this part; the reference has no fp8 path.
  * ---------------------------------------------------------------------- */

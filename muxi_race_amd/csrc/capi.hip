@@ -68,19 +68,19 @@ int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
 }
 
 // Rows per block of the align padding.  block_m != 0 is the caller's choice,
-// used by both stages.  0: pick_bm's size, except that 128 becomes 256 where a
-// 256-row item is faster for one stage and H is a multiple of 256 (measured):
-// Stage 1 of fp16 with >= 384 routed rows per expert on average (mixtral-like),
-// Stage 2 of fp8 with >= 192.  The other stage keeps 128-row items; those in
-// a block's empty second half end at once.  int8 keeps 128.
+// used by both stages.  0: pick_bm's size, except that 128 becomes 256 where
+// 256-row items are faster and H is a multiple of 256 (measured): fp16 with
+// >= 384 routed rows per expert on average (mixtral-like; Stage 1 only),
+// int8 and fp8 with >= 192 (Stage 1, and fp8's Stage 2).  A stage that keeps
+// 128-row items runs them over the same padding; those that fall in a block's
+// empty second half end at once.
 int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int qt, int64_t block_m) {
   if (block_m) return block_m;
   const int64_t bm = pick_bm(T, E, k);
   if (bm != 128 || H % 256) return bm;
   const int64_t avg = (T * k + E - 1) / E;
   if (qt == moe::kQF16) return avg >= 384 ? 256 : 128;
-  if (qt == moe::kQF8) return avg >= 192 ? 256 : 128;
-  return 128;
+  return avg >= 192 ? 256 : 128;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -280,14 +280,14 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
       (shared && (!aligned16(wg_s) || !aligned16(wu_s) || !aligned16(wd_s))))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
   const int64_t router_ws = w_router ? moe_router_workspace_bytes(T, H, E) : 0;
-  // a workspace sized for the 128-row padding (fp8 sized as int8) keeps it
+  // a workspace sized for the 128-row padding (block_m = 128) keeps it
   if (block_m == 256 && workspace_bytes < fused_layout(T, H, I, Ee, ke, 256, w8).total + router_ws) block_m = 128;
   const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, w8);
   const int64_t need = L.total + router_ws;
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
-  // rows per item of each stage: block_m, except over the 256-row padding,
-  // where one stage takes 256-row items (see align_bm)
-  const int64_t bm1 = block_m == 256 && qt == moe::kQF16 ? 256 : (block_m == 256 ? 128 : block_m);
+  // rows per item of each stage: block_m, except Stage 2 of fp16 and int8
+  // over the 256-row padding, which keeps 128-row items (see align_bm)
+  const int64_t bm1 = block_m;
   const int64_t bm2 = block_m == 256 && qt == moe::kQF8 ? 256 : (block_m == 256 ? 128 : block_m);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;

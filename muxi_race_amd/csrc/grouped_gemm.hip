@@ -130,7 +130,12 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 
   // 8-bit: the dequantisation scales of this lane's token rows and output
   // features, loaded before the K loop so that their latency hides behind it
-  // (padding rows read token 0's scale and are never stored).
+  // (padding rows read token 0's scale and are never stored).  The feature
+  // scales stay in registers only for wave tiles of up to two 32x32 blocks;
+  // larger tiles load them in the epilogue (registers would spill).
+  constexpr bool kHoistFeat = L::NBN * L::NBM <= 2;
+  const float* sgrow = I8 ? p.sg + (int64_t)e * p.I : nullptr;
+  const float* surow = I8 ? p.su + (int64_t)e * p.I : nullptr;
   float sxv[L::NBM];
   f32x4 sgv[L::NBN][4], suv[L::NBN][4];
   if constexpr (I8) {
@@ -143,16 +148,16 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       const bool valid = xr0 + 32 * b + (lq & 31) < actual;
       sxv[b] = p.x_scale[valid ? pid[b] / p.topk : 0];
     }
-    const float* sgrow = p.sg + (int64_t)e * p.I;
-    const float* surow = p.su + (int64_t)e * p.I;
+    if constexpr (kHoistFeat) {
 #pragma unroll
-    for (int a = 0; a < L::NBN; ++a)
+      for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (lq >> 5);
-        sgv[a][rg] = *reinterpret_cast<const f32x4*>(sgrow + n);
-        suv[a][rg] = *reinterpret_cast<const f32x4*>(surow + n);
-      }
+        for (int rg = 0; rg < 4; ++rg) {
+          const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (lq >> 5);
+          sgv[a][rg] = *reinterpret_cast<const f32x4*>(sgrow + n);
+          suv[a][rg] = *reinterpret_cast<const f32x4*>(surow + n);
+        }
+    }
   }
   Acc ag[L::NBN][L::NBM], au[L::NBN][L::NBM];
 #pragma unroll
@@ -268,10 +273,19 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
+          f32x4 gs, us;
+          if constexpr (kHoistFeat) {
+            gs = sgv[a][rg];
+            us = suv[a][rg];
+          } else {
+            const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
+            gs = *reinterpret_cast<const f32x4*>(sgrow + n);
+            us = *reinterpret_cast<const f32x4*>(surow + n);
+          }
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float g = ((float)ag[a][b][4 * rg + q] * sx) * sgv[a][rg][q];
-            const float u = ((float)au[a][b][4 * rg + q] * sx) * suv[a][rg][q];
+            const float g = ((float)ag[a][b][4 * rg + q] * sx) * gs[q];
+            const float u = ((float)au[a][b][4 * rg + q] * sx) * us[q];
             const float h = silu_mul(g, u);
             hv[b][a][4 * rg + q] = h;
             amax = fmaxf(amax, fabsf(h));
@@ -797,9 +811,10 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, int qt, bool g
       if (qt == kQF8) return go1<128, 2, NW, kQF8, true, false>(p, grid, s);
       return go1<128, 2, NW, kQF16, true, kPair>(p, grid, s);
     case 256:
-      // fp16, 256 token rows x (128 gate + 128 up) rows: two 64 KiB stages
-      if (qt == kQF16) return go1<256, 4, 8, kQF16, true, false>(p, grid, s);
-      return hipErrorInvalidValue;
+      // 256 token rows x (128 gate + 128 up) rows: two 64 KiB stages
+      if (qt == kQI8) return go1<256, 4, 8, kQI8, true, false>(p, grid, s);
+      if (qt == kQF8) return go1<256, 4, 8, kQF8, true, false>(p, grid, s);
+      return go1<256, 4, 8, kQF16, true, false>(p, grid, s);
   }
   return hipErrorInvalidValue;
 }

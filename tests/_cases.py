@@ -113,7 +113,7 @@ def moe_inputs(name, seed, device="cuda", T=None):
 
 def skewed_8bit_case(seed, device="cuda"):
     """T=800, H=512 (a multiple of 256), 200 routed rows per expert: 128-row
-    blocks picked, and the fp8 path pads experts to 256 rows.  Biases give an
+    blocks picked, and the 8-bit paths pad experts to 256 rows.  Biases give an
     empty expert, experts of <= 128 rows (an empty second half) and
     multi-block experts."""
     g = torch.Generator().manual_seed(seed)

@@ -77,10 +77,10 @@ def test_fp8_small(bm):
 
 
 def test_fp8_256_row_padding_ragged():
-    """fp8 Stage 2 runs 256-row items over the 256-row padding, Stage 1 128-row
-    items.  At T = 800 a few e4m3 boundary flips occur, so the oracle gates are
-    those of the large configs; against explicit 128-row blocks (same
-    intermediate codes, same K order per element) the output must agree."""
+    """Both fp8 stages run 256-row items over the 256-row padding.  At T = 800
+    a few e4m3 boundary flips occur, so the oracle gates are those of the large
+    configs; against explicit 128-row blocks (same K order per element) the
+    output must agree to within such flips."""
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     inp = skewed_8bit_case(76)
     _run(inp)
@@ -92,9 +92,10 @@ def test_fp8_256_row_padding_ragged():
     assert_close(a, b, atol=1e-3, rtol=1e-3, what="256-row padding vs 128-row blocks")
 
 
-def test_fp8_workspace_sized_as_int8_keeps_128_row_padding():
-    """A caller that sizes the fp8 workspace as int8's (w8a8 = 1) still gets a
-    correct result: the call falls back to the 128-row padding."""
+def test_fp8_workspace_sized_for_128_rows_keeps_128_row_padding():
+    """A caller that sizes the workspace for block_m = 128 and then passes
+    block_m = 0 still gets a correct result: the call keeps the 128-row
+    padding."""
     import ctypes
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     from muxi_race_amd._lib import lib
@@ -103,7 +104,7 @@ def test_fp8_workspace_sized_as_int8_keeps_128_row_padding():
     T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
     qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"], fmt="fp8")
     a = fused_moe(inp["x"], inp["logits"], None, None, None, k, expert_bias=inp["bias"], w8a8=qw)
-    small, full = L.moe_fused_workspace_bytes(T, H, I, E, k, 0, 1), L.moe_fused_workspace_bytes(T, H, I, E, k, 0, 2)
+    small, full = L.moe_fused_workspace_bytes(T, H, I, E, k, 128, 2), L.moe_fused_workspace_bytes(T, H, I, E, k, 0, 2)
     assert small < full
     ws = torch.empty(small, dtype=torch.uint8, device="cuda")
     b = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")

@@ -58,8 +58,8 @@ def test_w8a8_small(bm):
 
 
 def test_w8a8_skewed_ragged():
-    """int8 on the skewed 8-bit case (where fp8 pads experts to 256 rows, int8
-    keeps 128): an empty expert, partial and multi-block experts."""
+    """int8 over the 256-row padding (Stage 1 on 256-row items, Stage 2 on
+    128-row ones): an empty expert, partial and multi-block experts."""
     _run(skewed_8bit_case(22))
 
 

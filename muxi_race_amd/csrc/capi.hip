@@ -68,18 +68,18 @@ int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
 }
 
 // Rows per block of the align padding.  block_m != 0 is the caller's choice,
-// used by both stages.  0: pick_bm's size, except that 128 becomes 256 where
-// 256-row items are faster and H is a multiple of 256 (measured): fp16 with
-// >= 384 routed rows per expert on average (mixtral-like; Stage 1 only),
-// int8 and fp8 with >= 192 (Stage 1, and fp8's Stage 2).  A stage that keeps
-// 128-row items runs them over the same padding; those that fall in a block's
-// empty second half end at once.
+// used by both stages.  0: pick_bm's size, except that 128 becomes 256 when
+// experts hold >= 192 routed rows on average and H is a multiple of 256: then
+// Stage 1 runs 256-row items (and so does fp8's Stage 2), measured faster on
+// every format.  A stage that keeps 128-row items runs them over the same
+// padding; those that fall in a block's empty second half end at once.  At
+// fewer rows per expert half-empty 256-row blocks cost more than they save.
 int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int qt, int64_t block_m) {
+  (void)qt;
   if (block_m) return block_m;
   const int64_t bm = pick_bm(T, E, k);
   if (bm != 128 || H % 256) return bm;
   const int64_t avg = (T * k + E - 1) / E;
-  if (qt == moe::kQF16) return avg >= 384 ? 256 : 128;
   return avg >= 192 ? 256 : 128;
 }
 

@@ -123,7 +123,7 @@ def test_extreme_shapes(T, H, I, E, k):
 
 
 def test_256_row_padding_ragged():
-    """fp16 experts with >= 384 routed rows on average and H a multiple of 256:
+    """fp16 experts with >= 192 routed rows on average and H a multiple of 256:
     align pads experts to 256 rows, Stage 1 runs 256-row items, Stage 2
     128-row (paired) items.  Skewed biases give full, partial and empty
     256-row blocks, 128-row halves with no rows, and two empty experts."""

@@ -74,8 +74,7 @@ int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
 // every format.  A stage that keeps 128-row items runs them over the same
 // padding; those that fall in a block's empty second half end at once.  At
 // fewer rows per expert half-empty 256-row blocks cost more than they save.
-int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int qt, int64_t block_m) {
-  (void)qt;
+int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int64_t block_m) {
   if (block_m) return block_m;
   const int64_t bm = pick_bm(T, E, k);
   if (bm != 128 || H % 256) return bm;
@@ -228,8 +227,8 @@ int64_t moe_pick_block_m(int64_t T, int64_t E, int64_t k) { return pick_bm(T, E,
 int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                   int64_t block_m, int w8a8) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  // w8a8: 0 fp16, 1 int8, 2 fp8
-  block_m = align_bm(T, E, k, H, w8a8 == 0 ? moe::kQF16 : (w8a8 == 2 ? moe::kQF8 : moe::kQI8), block_m);
+  // w8a8: 0 fp16, nonzero 8-bit (1 int8, 2 fp8: one padding rule for both)
+  block_m = align_bm(T, E, k, H, block_m);
   return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
 }
 
@@ -258,7 +257,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   const int64_t Ee = E + (shared ? 1 : 0), ke = k + (shared ? 1 : 0);  // experts / choices incl. the shared one
   if (block_m != 0 && block_m != 32 && block_m != 64 && block_m != 128)
     return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {0,32,64,128}", (long long)block_m);
-  block_m = align_bm(T, shard ? E_route : Ee, ke, H, qt, block_m);
+  block_m = align_bm(T, shard ? E_route : Ee, ke, H, block_m);
   int rc = check_dims(T, H, I, shard ? E_route : Ee, ke, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
@@ -285,8 +284,9 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, w8);
   const int64_t need = L.total + router_ws;
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
-  // rows per item of each stage: block_m, except Stage 2 of fp16 and int8
-  // over the 256-row padding, which keeps 128-row items (see align_bm)
+  // rows per item of each stage: block_m, except that over the 256-row
+  // padding Stage 2 keeps 128-row (paired) items for fp16 and int8 (fp8
+  // takes 256-row ones; see align_bm)
   const int64_t bm1 = block_m;
   const int64_t bm2 = block_m == 256 && qt == moe::kQF8 ? 256 : (block_m == 256 ? 128 : block_m);
   hipStream_t s = (hipStream_t)stream;
@@ -398,7 +398,7 @@ int moe_fused_forward_hidden(const void* x, const void* w_router, const float* b
 int64_t moe_fused_shared_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                          int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  block_m = align_bm(T, E + 1, k + 1, H, moe::kQF16, block_m);
+  block_m = align_bm(T, E + 1, k + 1, H, block_m);
   return fused_layout(T, H, I, E + 1, k + 1, block_m, false).total + moe_router_workspace_bytes(T, H, E);
 }
 
@@ -419,7 +419,7 @@ int64_t moe_fused_ex_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                      int shared, int with_router) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   const int64_t s = shared ? 1 : 0;
-  block_m = align_bm(T, E + s, k + s, H, moe::kQF16, block_m);
+  block_m = align_bm(T, E + s, k + s, H, block_m);
   return fused_layout(T, H, I, E + s, k + s, block_m, false).total + (with_router ? moe_router_workspace_bytes(T, H, E) : 0);
 }
 
@@ -440,7 +440,7 @@ int moe_fused_forward_ex(const void* x, const float* logits, const void* w_route
 int64_t moe_fused_shard_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
                                         int64_t E_local, int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E_total <= 0 || E_local <= 0 || k <= 0) return 0;
-  block_m = align_bm(T, E_total, k, H, moe::kQF16, block_m);
+  block_m = align_bm(T, E_total, k, H, block_m);
   return fused_layout(T, H, I, E_local, k, block_m, false).total;
 }
 

@@ -20,31 +20,20 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Routes token t; logit(e) returns its logit for expert e (lane l asks for
-// experts l, l + 64, ...).  Lane j < k writes choice j to ids / wout at
-// t * kout + j; with e_shared >= 0, lane k appends the always-on shared
-// expert (id e_shared, weight 1) as choice k (kout = k + 1).
-template <int VPL, typename Logit>
-__device__ __forceinline__ void route_token_with(Logit&& logit, const float* __restrict__ bias, int t, int E,
-                                                 int k, int32_t* __restrict__ ids, float* __restrict__ wout,
-                                                 int kout = 0, int e_shared = -1) {
-  if (kout == 0) kout = k;
+// Routes token t from its logits v[j] = logit of expert l + 64 j (bias already
+// added; -inf where the expert is past E, `valid` bit j set otherwise).  Lane
+// j < k writes choice j to ids / wout at t * kout + j; with e_shared >= 0, lane
+// k appends the always-on shared expert (id e_shared, weight 1) as choice k
+// (kout = k + 1).
+template <int VPL>
+__device__ __forceinline__ void route_token_values(const float (&v)[VPL], uint32_t valid, int t, int k,
+                                                   int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                   int kout, int e_shared) {
   const int l = lane_id();
-  float v[VPL];
-  uint32_t valid = 0;
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int e = l + 64 * j;
-    v[j] = -INFINITY;
-    if (e < E) {
-      float x = logit(e);
-      if (bias) x = x + bias[e];
-      v[j] = x;
-      valid |= 1u << j;
-      m = fmaxf(m, x);
-    }
-  }
+  for (int j = 0; j < VPL; ++j)
+    if (valid & (1u << j)) m = fmaxf(m, v[j]);
   m = wave_max(m);
   float s = 0.0f;
 #pragma unroll
@@ -93,6 +82,29 @@ __device__ __forceinline__ void route_token_with(Logit&& logit, const float* __r
     ids[(int64_t)t * kout + k] = e_shared;
     wout[(int64_t)t * kout + k] = 1.0f;
   }
+}
+
+// Routes token t; logit(e) returns its logit for expert e (lane l asks for
+// experts l, l + 64, ...); kout as route_token_values (0: k).
+template <int VPL, typename Logit>
+__device__ __forceinline__ void route_token_with(Logit&& logit, const float* __restrict__ bias, int t, int E,
+                                                 int k, int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                 int kout = 0, int e_shared = -1) {
+  const int l = lane_id();
+  float v[VPL];
+  uint32_t valid = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = l + 64 * j;
+    v[j] = -INFINITY;
+    if (e < E) {
+      float x = logit(e);
+      if (bias) x = x + bias[e];
+      v[j] = x;
+      valid |= 1u << j;
+    }
+  }
+  route_token_values<VPL>(v, valid, t, k, ids, wout, kout == 0 ? k : kout, e_shared);
 }
 
 }  // namespace moe

@@ -111,9 +111,11 @@ __global__ __launch_bounds__(64 * NW) void router_gemm_kernel(const _Float16* __
   }
 }
 
-// Routing of the summed partials: one wave per token (route_token with a
-// logit loader that sums the ks_count splits in order); the summed logits are
-// also written to `logits` when it is not null.
+// Routing of the summed partials: one wave per token.  A lane sums the
+// ks_count splits of each of its VPL logits in split order; the loads of a
+// batch of 8 splits are issued for all VPL logits before any is summed, so a
+// lane has VPL * 8 loads in flight.  The summed logits are also written to
+// `logits` when it is not null.
 template <int VPL>
 __global__ __launch_bounds__(256) void route_partials_kernel(const float* __restrict__ part, int ks_count,
                                                              const float* __restrict__ bias, int T, int E,
@@ -122,24 +124,40 @@ __global__ __launch_bounds__(256) void route_partials_kernel(const float* __rest
                                                              float* __restrict__ logits, int e_shared) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // uniform per wave
-  // partials loaded 8 at a time (independent loads in flight), summed in split order
-  auto logit = [&](int e) {
-    constexpr int kBatch = 8;
-    const float* src = part + (int64_t)t * E + e;
-    const int64_t stride = (int64_t)T * E;
-    float v = 0.0f;
-    for (int s0 = 0; s0 < ks_count; s0 += kBatch) {
-      float pv[kBatch];
+  constexpr int kBatch = 8;
+  const int l = lane_id();
+  const float* src = part + (int64_t)t * E + l;
+  const int64_t stride = (int64_t)T * E;
+  float v[VPL];
+  uint32_t valid = 0;
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) pv[u] = s0 + u < ks_count ? src[(s0 + u) * stride] : 0.0f;
+  for (int j = 0; j < VPL; ++j) {
+    v[j] = 0.0f;
+    if (l + 64 * j < E) valid |= 1u << j;
+  }
+  for (int s0 = 0; s0 < ks_count; s0 += kBatch) {
+    float pv[VPL][kBatch];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
-        if (s0 + u < ks_count) v += pv[u];
+        pv[j][u] = (valid & (1u << j)) && s0 + u < ks_count ? src[(s0 + u) * stride + 64 * j] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (s0 + u < ks_count) v[j] += pv[j][u];
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (!(valid & (1u << j))) {
+      v[j] = -INFINITY;
+      continue;
     }
-    if (logits) logits[(int64_t)t * E + e] = v;
-    return v;
-  };
-  route_token_with<VPL>(logit, bias, t, E, k, ids, wout, e_shared >= 0 ? k + 1 : k, e_shared);
+    if (logits) logits[(int64_t)t * E + l + 64 * j] = v[j];
+    if (bias) v[j] = v[j] + bias[l + 64 * j];
+  }
+  route_token_values<VPL>(v, valid, t, k, ids, wout, e_shared >= 0 ? k + 1 : k, e_shared);
 }
 
 // Tile of the router GEMM: 128 tokens x MOE_ROUTER_BN experts (8 waves) when

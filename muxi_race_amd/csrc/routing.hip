@@ -120,6 +120,21 @@ __device__ __forceinline__ void align_place_range(const int32_t* __restrict__ id
   }
 }
 
+// Inclusive prefix sum over the wave's 64 lanes: Hillis-Steele inside each
+// 16-lane row with DPP row shifts (lanes shifted in from outside the row read
+// 0), then each row adds the totals of the rows before it (read from lanes 15,
+// 31, 47).  Integer adds, so the order of the terms does not matter.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+
 // Expert scan by one wave: tot[E] -> padded offsets pstart[E+1] in LDS, and
 // (when `out`) group sizes / offsets / padded offsets in global memory.
 __device__ __forceinline__ void align_expert_scan(const int* tot, int E, int BM, int* pstart, bool out,
@@ -131,15 +146,7 @@ __device__ __forceinline__ void align_expert_scan(const int* tot, int E, int BM,
     const int e = base + l;
     const int c = e < E ? tot[e] : 0;
     const int pc = (c + BM - 1) / BM * BM;
-    int ic = c, ip = pc;  // inclusive scans
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int a = __shfl_up(ic, o), b = __shfl_up(ip, o);
-      if (l >= o) {
-        ic += a;
-        ip += b;
-      }
-    }
+    const int ic = wave_inclusive_scan(c), ip = wave_inclusive_scan(pc);
     if (e < E) {
       pstart[e] = carry_p + ip - pc;
       if (out) {
@@ -148,8 +155,8 @@ __device__ __forceinline__ void align_expert_scan(const int* tot, int E, int BM,
         gpo[e] = carry_p + ip - pc;
       }
     }
-    carry += __shfl(ic, 63);
-    carry_p += __shfl(ip, 63);
+    carry += __builtin_amdgcn_readlane(ic, 63);
+    carry_p += __builtin_amdgcn_readlane(ip, 63);
   }
   if (l == 0) {
     pstart[E] = carry_p;

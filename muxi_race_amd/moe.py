@@ -26,6 +26,7 @@ __all__ = [
 ]
 
 _WORKSPACE: dict = {}
+_CAPTURED_RETIRED: list = []  # replaced buffers that captured graphs may still write
 
 
 def _ptr(t):
@@ -67,10 +68,20 @@ def _workspace(dev: torch.device, key, nbytes: int) -> torch.Tensor:
     """Scratch reused across calls, one per (device, stream, use): calls on
     different streams never share one (they may run concurrently), and a
     buffer is allocated on the stream that uses it, so replacing it by a
-    larger one is ordered after that stream's earlier kernels."""
-    k = (dev.index, torch.cuda.current_stream(dev).cuda_stream, key)
+    larger one is ordered after that stream's earlier kernels.
+
+    A call captured into a CUDA graph gets a buffer of its own (allocated
+    during the capture, cached apart from the eager ones): every replay of the
+    graph writes it, so an eager call that needs a larger buffer never frees
+    one a graph still uses.  A captured buffer that a later, larger capture
+    replaces is kept alive for the life of the process for the same reason.
+    Replays of graphs that share a buffer must not overlap."""
+    capturing = torch.cuda.is_current_stream_capturing()
+    k = (dev.index, torch.cuda.current_stream(dev).cuda_stream, capturing, key)
     buf = _WORKSPACE.get(k)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None and capturing:
+            _CAPTURED_RETIRED.append(buf)
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         _WORKSPACE[k] = buf
     return buf

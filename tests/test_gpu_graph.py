@@ -71,3 +71,37 @@ def test_router_and_shared_expert_replays():
     sh = [torch.randn(s, generator=g, device="cuda", dtype=torch.float16) * 0.02 for s in ((I, H), (I, H), (H, I))]
     _replays_match(lambda: fused_moe(inp["x"], None, inp["wg"], inp["wu"], inp["wd"], inp["k"],
                                      expert_bias=inp["bias"], router_weight=wr, shared_expert=sh))
+
+
+def test_capture_on_the_warm_stream_keeps_its_workspace():
+    """A graph captured on the stream the caller warmed up on keeps a
+    workspace of its own: an eager call on that stream that needs a larger one
+    does not free memory the graph's replays still write (tensors allocated
+    afterwards keep their values, and every replay still equals eager)."""
+    from muxi_race_amd import fused_moe
+    small = moe_inputs("small", 106, T=64)
+    big = moe_inputs("small", 107, T=2048)
+
+    def f_small():
+        return fused_moe(small["x"], small["logits"], small["wg"], small["wu"], small["wd"], small["k"])
+
+    eager = f_small().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        f_small()  # eager warm-up on the capture stream itself
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = f_small()
+        fused_moe(big["x"], big["logits"], big["wg"], big["wu"], big["wd"], big["k"])  # larger workspace
+        s.synchronize()
+        fill = [torch.full((32768,), 7.0, device="cuda") for _ in range(64)]  # reuse freed blocks
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager result"
+        assert all(bool((f == 7.0).all()) for f in fill), f"replay {i} wrote into freed memory"

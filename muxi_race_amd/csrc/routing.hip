@@ -259,12 +259,20 @@ __global__ __launch_bounds__(64 * NW) void align_place_kernel(
   int* before = pstart + E + 1;   // [E] pairs of expert e in the workgroups before this one
   const int tid = threadIdx.x, w = tid >> 6;
   const int G = gridDim.x, g = blockIdx.x;
+  // Every workgroup's count of expert e, loaded kBatch at a time before any is
+  // added, so one load latency is exposed per batch rather than per workgroup.
+  constexpr int kBatch = 16;
   for (int e = tid; e < E; e += 64 * NW) {
     int run = 0, mine = 0;
-    for (int v = 0; v < G; ++v) {
-      const int c = whist[(int64_t)v * E + e];
-      if (v == g) mine = run;
-      run += c;
+    for (int v0 = 0; v0 < G; v0 += kBatch) {
+      int c[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) c[u] = v0 + u < G ? whist[(int64_t)(v0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (v0 + u == g) mine = run;
+        run += c[u];
+      }
     }
     tot[e] = run;
     before[e] = mine;

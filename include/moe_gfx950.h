@@ -61,8 +61,19 @@ const char* moe_last_error_string(void);
  *   routed fp32|fp16 [V]  routing weights in raw (unpadded) order
  *   group_sizes int32 [E], group_offsets int32 [E+1],
  *   group_padded_offsets int32 [E+1], group_idx_for_bx int32 [nblk]
- *   out    fp16 [P, H]    written in full: rows of valid tokens get
+ *   out    fp16 [P, H]    rows of valid tokens get
  *          (silu(x Wg^T) * x Wu^T) Wd^T * routed, every other row gets 0.
+ *
+ * Block b = rows [128 b, 128 b + 128) belongs to expert e = group_idx_for_bx[b]
+ * (problem_detail.json:50 note 5; submission.py:1444): its first
+ * clamp(group_sizes[e] - (128 b - group_padded_offsets[e]), 0, 128) rows are
+ * valid, row i taking routed[clamp(group_offsets[e] + 128 b -
+ * group_padded_offsets[e] + i, 0, V - 1)] (submission.py:1286-1288).  The
+ * launch covers min(nblk, P / 128) blocks, as submission.py:2115 launches
+ * group_idx_for_bx.numel(): with nblk = P / 128 (the reference harness,
+ * remote_bench.py:82-101) `out` is written in full; rows past nblk blocks
+ * are left untouched.  A block whose gidx value lies outside [0, E) is
+ * written as 0.
  *
  * Requires H % 128 == 0, I % 128 == 0, P % 128 == 0.  `workspace` holds the
  * fp16 [P, I] intermediate; size it with moe_prerouted_workspace_bytes.

@@ -110,7 +110,6 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
                       const int32_t* group_idx_for_bx, void* out, int64_t P, int64_t H, int64_t I,
                       int64_t E, int64_t V, int64_t nblk, void* workspace, int64_t workspace_bytes,
                       void* stream) {
-  (void)group_idx_for_bx;  // block -> expert follows from group_padded_offsets
   if (P < 0 || H <= 0 || I <= 0 || E <= 0 || V < 0 || nblk < 0)
     return fail(MOE_ERR_INVALID_ARG, "bad sizes P=%lld H=%lld I=%lld E=%lld V=%lld", (long long)P, (long long)H, (long long)I, (long long)E, (long long)V);
   if (P == 0) return MOE_OK;  // nothing to write (submission.py:2117-2120)
@@ -120,14 +119,20 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   if (P * (H > I ? H : I) >= ((int64_t)1 << 40)) return fail(MOE_ERR_UNSUPPORTED, "problem too large");
   if (routed_dtype != MOE_ROUTED_F32 && routed_dtype != MOE_ROUTED_F16)
     return fail(MOE_ERR_INVALID_ARG, "routed_dtype=%d", routed_dtype);
-  if (!x || !w_gate || !w_up || !w_down || !group_sizes || !group_offsets || !group_padded_offsets || !out || (V > 0 && !routed))
+  if (!x || !w_gate || !w_up || !w_down || !group_sizes || !group_offsets || !group_padded_offsets || !out || (V > 0 && !routed) ||
+      (nblk > 0 && !group_idx_for_bx))
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) || !aligned16(out) || !aligned16(workspace))
     return fail(MOE_ERR_INVALID_ARG, "x, weights, out and workspace must be 16-byte aligned");
   if (workspace_bytes < moe_prerouted_workspace_bytes(P, I) || !workspace)
     return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)moe_prerouted_workspace_bytes(P, I));
   hipStream_t s = (hipStream_t)stream;
-  const int64_t blocks = P / 128;  // x, out and the workspace hold P rows
+  // Block b (rows [128 b, 128 b + 128)) belongs to expert group_idx_for_bx[b];
+  // the launch covers the gidx entries, as submission.py:2115 launches
+  // group_idx_for_bx.numel() blocks (rows past them are left untouched), and
+  // never more blocks than x, out and the workspace hold.
+  const int64_t blocks = nblk < P / 128 ? nblk : P / 128;
+  if (blocks == 0) return MOE_OK;
 
   moe::Stage1Params p1{};
   p1.x = (const char*)x;
@@ -136,6 +141,7 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p1.h = (char*)workspace;
   p1.gs = group_sizes;
   p1.gpo = group_padded_offsets;
+  p1.gidx = group_idx_for_bx;
   p1.topk = 1;
   p1.E = (int)E;
   p1.H = H;
@@ -152,6 +158,7 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p2.gs = group_sizes;
   p2.go = group_offsets;
   p2.gpo = group_padded_offsets;
+  p2.gidx = group_idx_for_bx;
   p2.E = (int)E;
   p2.H = H;
   p2.I = I;

@@ -74,8 +74,12 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 
   const int nt = (int)(p.I / kBN);
   Work w;
-  if (!schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w)) return;
+  // gathered (fused) launches follow the align metadata; direct (pre-routed)
+  // ones map block -> expert through gidx
+  if (GATHER ? !schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w)
+             : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, kBN, nt, PAIR, w)) return;
   const int e = w.e;
+  if (e < 0) return;  // a block owned by no expert: Stage 2 writes its rows as 0
   const int gpo_e = p.gpo[e];
   const int row0 = w.row0;
   const int n0 = w.n0;
@@ -475,7 +479,10 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 
   const int nt = (int)(p.H / BN);
   Work w;
-  if (!schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, !FUSED, PAIR, w)) return;
+  // fused launches follow the align metadata; pre-routed ones map block ->
+  // expert through gidx (every block of the launch is an item)
+  if (FUSED ? !schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, false, PAIR, w)
+            : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, BN, nt, PAIR, w)) return;
   const int row0 = w.row0;
   const int n0 = w.n0;
   const int rx = PAIR ? w.rows : BM;  // token rows of the tile (stage rows [0, rx))

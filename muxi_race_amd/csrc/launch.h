@@ -25,6 +25,7 @@ struct Stage1Params {
   const int32_t* gs;        // [E]
   const int32_t* gpo;       // [E+1]
   const int32_t* sorted_ids;  // gather only: [padded rows], sentinel = T*topk
+  const int32_t* gidx;      // direct only: block -> expert ([host_blocks] entries)
   const char* wg_shared;    // weights of expert e_shared ([I, H]) when e_shared >= 0
   const char* wu_shared;
   int e_shared = -1;        // always-on shared expert's index, or -1
@@ -35,7 +36,8 @@ struct Stage1Params {
   int E;
   int64_t H;
   int64_t I;
-  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher)
+  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher);
+                            // direct: blocks of the launch (gidx entries, clamped)
 };
 
 // Stage 2: y = h Wd^T, scaled by the routing weight of each row.
@@ -52,6 +54,7 @@ struct Stage2Params {
   const int32_t* go;
   const int32_t* gpo;
   const int32_t* sorted_ids;  // fused only
+  const int32_t* gidx;      // pre-routed only: block -> expert ([host_blocks] entries)
   const char* wd_shared;    // down weights of expert e_shared ([H, I]) when e_shared >= 0
   int e_shared = -1;        // always-on shared expert's index, or -1
   int64_t a_ld = 0;         // bytes between rows of a (0: I elements)
@@ -61,7 +64,8 @@ struct Stage2Params {
   int64_t H;
   int64_t I;
   int64_t V;                // pre-routed: entries of `routed` (raw index is clamped to V-1)
-  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher)
+  int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher);
+                            // pre-routed: blocks of the launch (gidx entries, clamped)
 };
 
 // qt: a QuantType

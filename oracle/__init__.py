@@ -23,6 +23,10 @@ Pinning (how each function is checked independently of its own formula):
                            loop on tiny inputs, E=1 dense SwiGLU, zero-size
                            experts, V=0, NaN-poisoned padding, power-of-two
                            linearity (tests/test_oracle_core.py).
+* ``prerouted_forward_blocks`` -- equals ``prerouted_forward`` on harness
+                           metadata (random splits); hand-derived answers for
+                           swapped / trailing / out-of-range / short gidx
+                           (tests/test_oracle_blocks.py).
 * ``combine``           -- closed form on one-hot inputs (tests/test_oracle_core.py).
 * ``quantize_rows_int8`` / ``w8a8_forward`` -- exact integer checks on
                            hand-made rows, round-half-away edge cases, and the
@@ -45,6 +49,7 @@ from .moe_ref import (  # noqa: F401
     align,
     metadata_from_group_sizes,
     prerouted_forward,
+    prerouted_forward_blocks,
     gather_rows,
     combine,
     fused_moe_forward,

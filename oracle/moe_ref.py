@@ -162,6 +162,51 @@ def prerouted_forward(x, w_gate, w_up, w_down, routed, group_sizes, group_offset
     return out if out_fp32 else out.to(torch.float16)
 
 
+def prerouted_forward_blocks(x, w_gate, w_up, w_down, routed, group_sizes, group_offsets,
+                             group_padded_offsets, group_idx_for_bx, out=None, block_m: int = 128):
+    """The reference operator's per-block form (submission.py:1444-1447,
+    :1283-1299, :2115): the launch covers nblk = min(len(group_idx_for_bx),
+    P // block_m) blocks; block b is expert e = group_idx_for_bx[b], with
+    token offset o = b*block_m - gpo[e] and clamp(gs[e] - o, 0, block_m)
+    valid rows; valid row i is the SwiGLU MLP of x's row times
+    routed[clamp(go[e] + o + i, 0, V - 1)]; the block's other rows are 0.
+    A block whose expert lies outside [0, E) is all 0 (the build's rule: the
+    reference would read out of bounds).  Rows past the launched blocks keep
+    ``out``'s contents (zeros when ``out`` is None).  Returns float16 [P, H].
+    With group metadata from ``metadata_from_group_sizes`` this equals
+    ``prerouted_forward`` (the problem_detail.json:50 loop)."""
+    x = _as_t(x)
+    P, H = x.shape
+    res = torch.zeros((P, H), dtype=torch.float16) if out is None else _as_t(out).to(torch.float16).clone()
+    gs = [int(v) for v in _as_t(group_sizes).tolist()]
+    go = [int(v) for v in _as_t(group_offsets).tolist()]
+    gpo = [int(v) for v in _as_t(group_padded_offsets).tolist()]
+    gidx = [int(v) for v in _as_t(group_idx_for_bx).tolist()]
+    routed = _as_t(routed).float()
+    V = routed.numel()
+    E = len(gs)
+    nblk = min(len(gidx), P // block_m)
+    wcache = {}
+    for b in range(nblk):
+        r0 = b * block_m
+        blk = torch.zeros((block_m, H), dtype=torch.float32)
+        e = gidx[b]
+        if 0 <= e < E:
+            o = r0 - gpo[e]
+            n = max(0, min(block_m, gs[e] - o))
+            if n:
+                if e not in wcache:
+                    wcache[e] = tuple(_as_t(w[e]).float() for w in (w_gate, w_up, w_down))
+                wg, wu, wd = wcache[e]
+                xe = x[r0 : r0 + n].float()
+                h = silu_mul(xe @ wg.T, xe @ wu.T)
+                idx = torch.clamp(torch.arange(n) + (go[e] + o), 0, max(V - 1, 0))
+                scale = routed[idx] if V else torch.zeros(n)
+                blk[:n] = (h @ wd.T) * scale.unsqueeze(1)
+        res[r0 : r0 + block_m] = blk.to(torch.float16)
+    return res
+
+
 def gather_rows(x, sorted_pair_ids, top_k: int):
     """Expert-sorted activation rows: row r <- x[sorted_pair_ids[r] // top_k].
 
@@ -340,7 +385,7 @@ def _int_matmul(a: np.ndarray, b_t: np.ndarray) -> np.ndarray:
 def _exact_matmul(a: np.ndarray, b_t: np.ndarray) -> np.ndarray:
     """a @ b_t.T in float64 for 8-bit operand values (int8 or e4m3): exact,
     as the integer or 2**-18-grid sums stay below 2**53 ulps."""
-    return a.astype(np.float64) @ b_t.astype(np.float64).T
+    return np.asarray(a, dtype=np.float64) @ np.asarray(b_t, dtype=np.float64).T
 
 
 def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k: int,

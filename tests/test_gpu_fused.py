@@ -1,12 +1,16 @@
 """GPU parity of fused_moe (route -> align -> Stage1 -> Stage2 -> combine)
-against the CPU oracle, on every BASELINE config.  Full-size configs are
-checked on a seeded sample of tokens: tokens are independent, so the oracle
-run on the sampled rows (with the full expert weights) is exact for them."""
+against the CPU oracle, on every BASELINE config.  Every call writes into a
+NaN-poisoned output that must come back finite everywhere.  Full-size configs
+are checked on a stratified token set (tests/_cases.py stratified_tokens):
+the first and last pair of every touched expert and the first row of every
+block, so every item of both stages feeds a checked element; tokens are
+independent, so the oracle on those rows (with the full expert weights) is
+exact for them."""
 import numpy as np
 import pytest
 import torch
 
-from _cases import moe_inputs
+from _cases import moe_inputs, stratified_tokens
 from conftest import assert_close
 from oracle import fused_moe_forward, route_topk
 
@@ -15,22 +19,25 @@ pytestmark = pytest.mark.gpu
 
 def _gpu(inp, block_m=0):
     from muxi_race_amd import fused_moe
+    out = torch.full((inp["T"], inp["H"]), float("nan"), dtype=torch.float16, device="cuda")
     out, (ids, w) = fused_moe(inp["x"], inp["logits"], inp["wg"], inp["wu"], inp["wd"], inp["k"],
-                              expert_bias=inp["bias"], block_m=block_m, return_routing=True)
+                              expert_bias=inp["bias"], block_m=block_m, return_routing=True, out=out)
     torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
     return out, ids, w
 
 
-def _check(inp, sample=None, block_m=0, what=""):
+def _check(inp, sample=None, block_m=0, what="", **strat):
+    """sample None: every token; "strat": stratified_tokens(**strat)."""
     out, ids, w = _gpu(inp, block_m)
     T = inp["T"]
-    rows = torch.arange(T) if sample is None else torch.from_numpy(
-        np.sort(np.random.default_rng(T).choice(T, sample, replace=False)))
     bias = None if inp["bias"] is None else inp["bias"].cpu()
     # routing indices are bit-exact for every token
     rid, rw = route_topk(inp["logits"].cpu().numpy(), inp["k"], None if bias is None else bias.numpy())
     np.testing.assert_array_equal(ids.cpu().numpy(), rid)
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    rows = torch.arange(T) if sample is None else torch.from_numpy(stratified_tokens(rid, seed=T, **strat))
+    print(f"{what}: {len(rows)} of {T} tokens checked", flush=True)
     ref = fused_moe_forward(inp["x"][rows.cuda()].cpu(), inp["logits"][rows.cuda()].cpu(),
                             inp["wg"], inp["wu"], inp["wd"], inp["k"], bias)
     assert_close(out[rows.cuda()], ref, what=what)
@@ -52,16 +59,16 @@ def test_decode_full():
 
 
 def test_mixtral_sampled():
-    _check(moe_inputs("mixtral", 4), sample=24, what="mixtral")
+    _check(moe_inputs("mixtral", 4), sample="strat", what="mixtral")
 
 
 def test_mixtral_ragged():
     # H = 4096 takes Stage 2's 256-wide N tiles; T = 700 leaves ragged last blocks
-    _check(moe_inputs("mixtral", 9, T=700), sample=40, block_m=128, what="mixtral T=700")
+    _check(moe_inputs("mixtral", 9, T=700), sample="strat", block_m=128, what="mixtral T=700")
 
 
 def test_dsv3_sampled():
-    _check(moe_inputs("dsv3", 5), sample=8, what="dsv3")
+    _check(moe_inputs("dsv3", 5), sample="strat", what="dsv3")
 
 
 def test_edge_single_token_and_single_expert():
@@ -147,4 +154,4 @@ def test_large_batch_sampled():
     """A large prefill batch: dsv3 shape at T = 32768 (262144 routed pairs, the
     64-workgroup align, 3.8 GB of per-pair rows), checked on sampled tokens."""
     inp = moe_inputs("dsv3", 12, T=32768)
-    _check(inp, sample=6, what="dsv3 T=32768")
+    _check(inp, sample="strat", what="dsv3 T=32768", max_block_starts=256, extra=32)

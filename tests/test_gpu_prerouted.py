@@ -121,3 +121,55 @@ def test_rejects_bad_metadata_dtype():
     args[5] = args[5].long()
     with pytest.raises(TypeError):
         run_kernel(*args, torch.empty_like(args[0]))
+
+
+def _meta_tensors(sizes, go, gpo, gidx, dev="cuda"):
+    return [torch.tensor(list(a), dtype=torch.int32, device=dev) for a in (sizes, go, gpo, gidx)]
+
+
+def _block_case(sizes, go, gpo, gidx, P, H, I, seed, V=None):
+    g = torch.Generator().manual_seed(seed)
+    E = len(sizes)
+    x = torch.randn(P, H, generator=g).half().cuda()
+    ws = [(torch.randn(shape, generator=g) * 0.05).half().cuda() for shape in ((E, I, H), (E, I, H), (E, H, I))]
+    routed = torch.rand(int(go[-1]) if V is None else V, generator=g).cuda()
+    return [x, *ws, routed, *_meta_tensors(sizes, go, gpo, gidx)]
+
+
+@pytest.mark.parametrize("name,sizes,go,gpo,gidx,P", [
+    # two trailing blocks past gpo[E] naming the last expert: their rows are 0
+    ("trailing", [3, 300], [0, 3, 303], [0, 128, 512], [0, 1, 1, 1, 1, 1], 6 * 128),
+    # gidx one block shorter than P: the last block is left untouched
+    ("short", [3, 300], [0, 3, 303], [0, 128, 512], [0, 1, 1, 1], 5 * 128),
+    # swapped experts: block 0 runs expert 1 at token offset -128
+    ("swapped", [128, 128], [0, 128, 256], [0, 128, 256], [1, 0], 256),
+    # non-monotone runs (pairs form inside each run) and an out-of-range value
+    ("runs", [256, 384, 100], [0, 256, 640, 740], [0, 256, 640, 768],
+     [0, 0, 1, 1, 1, 2, 0, 0, 9], 9 * 128),
+])
+def test_group_idx_for_bx_maps_blocks(name, sizes, go, gpo, gidx, P):
+    """Block b runs expert group_idx_for_bx[b] over min(nblk, P / 128) blocks
+    (problem_detail.json:50 note 5; submission.py:1444, :2115), against the
+    oracle's per-block form; rows past the launched blocks keep their NaN."""
+    from oracle import prerouted_forward_blocks
+    args = _block_case(sizes, go, gpo, gidx, P, 256, 384, seed=len(name))
+    out = _run(args)
+    nan_init = torch.full((P, 256), float("nan"), dtype=torch.float16)
+    ref = prerouted_forward_blocks(*[a.cpu() for a in args], out=nan_init)
+    launched = min(len(gidx), P // 128) * 128
+    assert_close(out[:launched], ref[:launched], what=f"gidx {name}")
+    assert torch.isnan(out[launched:].float()).all()
+    if name == "trailing":
+        assert (out[512:] == 0).all()
+
+
+def test_group_idx_for_bx_equals_expert_loop_on_harness_metadata():
+    """On remote_bench.py:82-101 metadata the per-block map is the expert loop:
+    the two oracles agree and the GPU matches both (multi-block experts pair)."""
+    from oracle import prerouted_forward_blocks
+    sizes = [0, 700, 1, 128, 129, 255]
+    args = prerouted_inputs(sizes, 512, 256, seed=31, init="ns")
+    out = _run(args)
+    ref = prerouted_forward(*args)
+    assert torch.equal(ref, prerouted_forward_blocks(*[a.cpu() for a in args]))
+    assert_close(out, ref, what="harness metadata")

@@ -1,16 +1,25 @@
 """GPU W8A8: quantiser bit-exact against the oracle; fused W8A8 elementwise
 against the W8A8 oracle (same quantised arithmetic) and within the north-star
-gate (relative L2 <= 5e-2) against the fp16 oracle."""
+gate (relative L2 <= 5e-2) against the fp16 oracle.
+
+Elementwise against the fp16 oracle the W8A8 path is reported, not gated at
+100%: per-row weight and per-token activation int8 at H = 7168 leave ~2.4%
+relative L2, and about 13% of elements fall outside |d| <= 1e-2 + 5e-2 |ref|
+(a property of the quantisation scheme, the same for the oracle's own W8A8
+arithmetic).  The fraction inside is printed and held above 0.80.
+Full-size outputs are NaN-poisoned and must come back finite; the w8a8
+config is checked on a stratified token set (tests/_cases.py)."""
 import numpy as np
 import pytest
 import torch
 
-from _cases import moe_inputs, skewed_8bit_case
+from _cases import moe_inputs, scale_contrast_case, skewed_8bit_case, stratified_tokens
 from conftest import assert_close
-from oracle import fused_moe_forward, quantize_rows_int8, w8a8_forward
+from oracle import fused_moe_forward, quantize_rows_int8, route_topk, w8a8_forward
 
 pytestmark = pytest.mark.gpu
 W8A8_REL_L2 = 5e-2
+W8A8_ELEMENTWISE_FLOOR = 0.80  # fraction within 1e-2 + 5e-2 |ref| of the fp16 oracle
 
 
 @pytest.mark.parametrize("K", [1024, 2048 + 8, 7168, 8200])  # register path (4, 8, 16 chunks) and two-pass
@@ -32,23 +41,32 @@ def test_quantize_rows_bit_exact(K):
 def _run(inp, sample=None, block_m=0):
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     qw = quantize_w8a8_weights(inp["wg"], inp["wu"], inp["wd"])
-    out = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw,
-                    block_m=block_m)
-    torch.cuda.synchronize()
     T = inp["T"]
-    rows = torch.arange(T) if sample is None else torch.from_numpy(
-        np.sort(np.random.default_rng(T).choice(T, sample, replace=False)))
+    out = torch.full((T, inp["H"]), float("nan"), dtype=torch.float16, device="cuda")
+    out = fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw,
+                    block_m=block_m, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
+    bias = None if inp["bias"] is None else inp["bias"].cpu()
+    if sample is None:
+        rows = torch.arange(T)
+    else:
+        rid, _ = route_topk(inp["logits"].cpu().numpy(), inp["k"], None if bias is None else bias.numpy())
+        rows = torch.from_numpy(stratified_tokens(rid, seed=T))
     r = rows.cuda()
     x, lg = inp["x"][r].cpu(), inp["logits"][r].cpu()
-    bias = None if inp["bias"] is None else inp["bias"].cpu()
     ref8 = w8a8_forward(x, lg, qw.q_gate.cpu().numpy(), qw.s_gate.cpu().numpy(), qw.q_up.cpu().numpy(),
                         qw.s_up.cpu().numpy(), qw.q_down.cpu().numpy(), qw.s_down.cpu().numpy(),
                         inp["k"], bias)
-    ref16 = fused_moe_forward(x, lg, inp["wg"], inp["wu"], inp["wd"], inp["k"], bias)
+    ref16 = fused_moe_forward(x, lg, inp["wg"], inp["wu"], inp["wd"], inp["k"], bias).float()
     got = out[r].float().cpu()
     assert_close(got, ref8, what="w8a8 vs w8a8 oracle")
-    rel = float((got - ref16.float()).norm() / ref16.float().norm())
+    rel = float((got - ref16).norm() / ref16.norm())
+    inside = float(((got - ref16).abs() <= 1e-2 + 5e-2 * ref16.abs()).float().mean())
+    print(f"w8a8 vs fp16 oracle on {len(rows)} tokens: rel L2 {rel:.4f}, "
+          f"{inside:.4f} of elements within 1e-2 + 5e-2|ref|", flush=True)
     assert rel < W8A8_REL_L2, f"relative L2 vs fp16 oracle {rel:.4f}"
+    assert inside >= W8A8_ELEMENTWISE_FLOOR, f"only {inside:.4f} of elements within 1e-2 + 5e-2|ref|"
     return rel
 
 
@@ -64,4 +82,24 @@ def test_w8a8_skewed_ragged():
 
 
 def test_w8a8_config_sampled():
-    _run(moe_inputs("w8a8", 22), sample=16)
+    _run(moe_inputs("w8a8", 22), sample="strat")
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_intermediate_scale_blocks(fmt):
+    """I = 256 with h's second 128-column block ~1000x its first (the oracle's
+    scale-contrast case): the GPU keeps the small block (per-block scales) and
+    matches the 8-bit oracle elementwise."""
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    from oracle import quantize_rows_fp8
+    qfn = quantize_rows_int8 if fmt == "int8" else quantize_rows_fp8
+    x, lg, wg, wu, wd, ref, _, k = scale_contrast_case(qfn)
+    qw = quantize_w8a8_weights(wg.cuda(), wu.cuda(), wd.cuda(), fmt=fmt)
+    out = fused_moe(x.cuda(), lg.cuda(), None, None, None, k, w8a8=qw).float().cpu()
+    torch.cuda.synchronize()
+    codes = lambda t: (t.view(torch.uint8) if fmt == "fp8" else t).cpu().numpy()
+    ref8 = w8a8_forward(x, lg, codes(qw.q_gate), qw.s_gate.cpu().numpy(), codes(qw.q_up), qw.s_up.cpu().numpy(),
+                        codes(qw.q_down), qw.s_down.cpu().numpy(), k, fmt=fmt).float()
+    assert_close(out, ref8, what=f"{fmt} scale contrast vs oracle")
+    rel0 = float((out[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
+    assert rel0 < (5e-2 if fmt == "int8" else 8e-2), rel0

@@ -4,6 +4,7 @@ the north-star gate against the fp16 oracle."""
 import numpy as np
 import torch
 
+from _cases import scale_contrast_case
 from oracle import fused_moe_forward, quantize_rows_int8, w8a8_forward
 from oracle.moe_ref import _int_matmul
 
@@ -92,3 +93,23 @@ def test_w8a8_exact_on_representable_inputs():
     # only the intermediate requantisation remains (h = silu(g)*g is heavy
     # tailed, ~1.3% here): error well under the gate
     assert float((out - ref).norm() / ref.norm()) < 2e-2
+
+
+def test_w8a8_intermediate_scale_is_per_128_columns():
+    """Per-(row, 128-column) intermediate scales keep the small block: out[:, 0]
+    stays within 5% of the fp16 oracle.  One scale per row would quantise the
+    small block (|h| < amax / 254) to 0 and give out[:, 0] = 0 exactly; taking
+    the scales in the wrong block order would multiply it by ~1000."""
+    x, lg, wg, wu, wd, ref, q, k = scale_contrast_case(quantize_rows_int8)
+    (qg, sg), (qu, su), (qd, sd) = q
+    out = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k).float()
+    h_small = ref[:, 0].abs()
+    assert (h_small > 1e-3).all(), "the small block contributes"
+    big = ref[:, 1].abs().mean() / ref[:, 0].abs().mean()
+    assert big > 300, f"block contrast only {float(big):.0f}x"
+    rel0 = float((out[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
+    rel1 = float((out[:, 1] - ref[:, 1]).norm() / ref[:, 1].norm())
+    assert rel0 < 5e-2 and rel1 < 5e-2, (rel0, rel1)
+    # the same data with one scale over both blocks loses the small block
+    out_row = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k, scale_block=256).float()
+    assert float(out_row[:, 0].abs().max()) == 0.0

@@ -147,6 +147,22 @@ int moe_fused_forward(const void* x, const float* logits, const float* bias,
                       void* workspace, int64_t workspace_bytes,
                       int32_t* topk_ids_out, float* topk_weights_out, void* stream);
 
+/* Allocation-free variant of moe_fused_forward.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and result as moe_fused_forward without the workspace: the
+ * library keeps a static 64 MiB scratch array per GPU (held until the process
+ * ends) and calls no allocator.  That fits decode-sized batches (e.g. T up to
+ * ~200 at H 7168, I 2048, E 256, top-8); a problem whose fused workspace
+ * (moe_fused_workspace_bytes with w8a8 = 0) exceeds 64 MiB returns
+ * MOE_ERR_WORKSPACE.  The scratch of the current device is used (`stream`
+ * must belong to it); every call on one GPU shares it, so calls that overlap
+ * on one GPU (other streams, other threads) race. */
+int moe_fused_forward_noalloc(const void* x, const float* logits, const float* bias,
+                              const void* w_gate, const void* w_up, const void* w_down, void* out,
+                              int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t block_m,
+                              int32_t* topk_ids_out, float* topk_weights_out, void* stream);
+
 /* Measurement variant of moe_fused_forward (no counterpart in the reference):
  * stage_events, when not NULL, holds 7 hipEvent_t (entries may be NULL) that
  * are recorded on `stream` at the start and after routing, alignment,

@@ -48,6 +48,8 @@ SIGNATURES = {
     "moe_pick_block_m": (_i64, [_i64, _i64, _i64]),
     "moe_fused_forward": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _p, _i64, _p, _p, _p]),
+    "moe_fused_forward_noalloc": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _p, _p, _p]),
     "moe_fused_forward_events": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                         _i64, _i64, _p, _i64, _p, _p, _p, _p]),
     "moe_quantize_rows_w8": (_int, [_p, _i64, _i64, _p, _p, _p]),

@@ -8,6 +8,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -460,6 +462,75 @@ int moe_fused_forward_shard(const void* x, const float* logits, const float* bia
   return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr,
                       nullptr, nullptr, nullptr, expert_begin, E_total, out, T, H, I, E_local, k, block_m, workspace,
                       workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused forward.  Its workspace is `scratch`, a static device
+// array that every GPU the library runs on holds (one copy per device, at its
+// own address) until the process ends.  Host code never uses the array's name
+// as an address: at a device's first call, with that device current,
+// hipGetSymbolAddress gives that device's copy, kept in g_scratch_ptr.
+// Nothing in the fused workspace has to start at zero (every piece is fully
+// written before it is read), so the array is never cleared; it keeps the
+// last call's contents.  Calls that overlap on one GPU share the array and
+// race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kNoAllocScratchBytes = (int64_t)64 << 20;  // 64 MiB per GPU
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// This device's copy of `scratch` (looked up once per device).
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MOE_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MOE_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MOE_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+
+extern "C" {
+
+int moe_fused_forward_noalloc(const void* x, const float* logits, const float* bias, const void* w_gate,
+                              const void* w_up, const void* w_down, void* out, int64_t T, int64_t H,
+                              int64_t I, int64_t E, int64_t k, int64_t block_m, int32_t* topk_ids_out,
+                              float* topk_weights_out, void* stream) {
+  if (block_m != 0 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(MOE_ERR_UNSUPPORTED, "block_m=%lld not in {0,32,64,128}", (long long)block_m);
+  int64_t bm = align_bm(T, E, k, H, block_m);
+  int rc = check_dims(T, H, I, E, k, bm);
+  if (rc) return rc;
+  if (T == 0) return MOE_OK;
+  // the padding the call will use: 256-row blocks only where they fit (as
+  // for any workspace sized for 128-row blocks)
+  int64_t need = fused_layout(T, H, I, E, k, bm, false).total;
+  if (bm == 256 && need > kNoAllocScratchBytes) need = fused_layout(T, H, I, E, k, 128, false).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(MOE_ERR_WORKSPACE,
+                "moe_fused_forward_noalloc: T=%lld H=%lld I=%lld E=%lld k=%lld needs %lld bytes of scratch, the "
+                "static scratch holds %lld; pass a workspace to moe_fused_forward instead",
+                (long long)T, (long long)H, (long long)I, (long long)E, (long long)k, (long long)need,
+                (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device(&ws))) return rc;
+  return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, 0, 0, out, T, H, I, E, k, block_m, ws, kNoAllocScratchBytes,
+                      topk_ids_out, topk_weights_out, stream, nullptr);
 }
 
 int moe_fused_forward_events(const void* x, const float* logits, const float* bias,

@@ -86,6 +86,19 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
                       void* out, int64_t P, int64_t H, int64_t I, int64_t E, int64_t V,
                       int64_t nblk, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Measurement variant of moe_run_prerouted (no counterpart in the reference):
+ * stage_events, when not NULL, holds 3 hipEvent_t (entries may be NULL)
+ * recorded on `stream` at the start, after Stage 1 and after Stage 2, so a
+ * caller can time each kernel on the stream it runs on (the reference's
+ * remote_bench.py:196-228 --phase split). */
+int moe_run_prerouted_events(const void* x, const void* w_gate, const void* w_up, const void* w_down,
+                             const void* routed, int routed_dtype,
+                             const int32_t* group_sizes, const int32_t* group_offsets,
+                             const int32_t* group_padded_offsets, const int32_t* group_idx_for_bx,
+                             void* out, int64_t P, int64_t H, int64_t I, int64_t E, int64_t V,
+                             int64_t nblk, void* workspace, int64_t workspace_bytes, void* stream,
+                             void* const* stage_events);
+
 /* ------------------------------------------------------------------------
  * Router: v = logits (+ bias), fp32 [T, E]; ids = the k largest v per row in
  * descending order, ties to the lower expert index; weights = softmax(v) at

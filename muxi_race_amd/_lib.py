@@ -26,6 +26,8 @@ SIGNATURES = {
     "moe_prerouted_workspace_bytes": (_i64, [_i64, _i64]),
     "moe_run_prerouted": (_int, [_p, _p, _p, _p, _p, _int, _p, _p, _p, _p, _p,
                                  _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p]),
+    "moe_run_prerouted_events": (_int, [_p, _p, _p, _p, _p, _int, _p, _p, _p, _p, _p,
+                                        _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _p]),
     "moe_route_topk": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "moe_align_capacity_rows": (_i64, [_i64, _i64, _i64, _i64]),
     "moe_align_scratch_bytes": (_i64, [_i64, _i64, _i64]),

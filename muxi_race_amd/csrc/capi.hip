@@ -106,12 +106,12 @@ const char* moe_last_error_string(void) { return g_err; }
 
 int64_t moe_prerouted_workspace_bytes(int64_t P, int64_t I) { return P > 0 && I > 0 ? P * I * 2 : 0; }
 
-int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const void* w_down,
-                      const void* routed, int routed_dtype, const int32_t* group_sizes,
-                      const int32_t* group_offsets, const int32_t* group_padded_offsets,
-                      const int32_t* group_idx_for_bx, void* out, int64_t P, int64_t H, int64_t I,
-                      int64_t E, int64_t V, int64_t nblk, void* workspace, int64_t workspace_bytes,
-                      void* stream) {
+int moe_run_prerouted_events(const void* x, const void* w_gate, const void* w_up, const void* w_down,
+                             const void* routed, int routed_dtype, const int32_t* group_sizes,
+                             const int32_t* group_offsets, const int32_t* group_padded_offsets,
+                             const int32_t* group_idx_for_bx, void* out, int64_t P, int64_t H, int64_t I,
+                             int64_t E, int64_t V, int64_t nblk, void* workspace, int64_t workspace_bytes,
+                             void* stream, void* const* stage_events) {
   if (P < 0 || H <= 0 || I <= 0 || E <= 0 || V < 0 || nblk < 0)
     return fail(MOE_ERR_INVALID_ARG, "bad sizes P=%lld H=%lld I=%lld E=%lld V=%lld", (long long)P, (long long)H, (long long)I, (long long)E, (long long)V);
   if (P == 0) return MOE_OK;  // nothing to write (submission.py:2117-2120)
@@ -148,8 +148,12 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p1.E = (int)E;
   p1.H = H;
   p1.I = I;
+  // optional stage markers: ev[0] start, [1] stage 1, [2] stage 2
+  auto mark = [&](int i) { if (stage_events && stage_events[i]) (void)hipEventRecord((hipEvent_t)stage_events[i], s); };
+  mark(0);
   int rc = check_launch(moe::launch_stage1(p1, 128, moe::kQF16, false, blocks, s), "stage1");
   if (rc) return rc;
+  mark(1);
 
   moe::Stage2Params p2{};
   p2.a = (const char*)workspace;
@@ -165,7 +169,20 @@ int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const
   p2.H = H;
   p2.I = I;
   p2.V = V;
-  return check_launch(moe::launch_stage2(p2, 128, moe::kQF16, false, blocks, s), "stage2");
+  rc = check_launch(moe::launch_stage2(p2, 128, moe::kQF16, false, blocks, s), "stage2");
+  mark(2);
+  return rc;
+}
+
+int moe_run_prerouted(const void* x, const void* w_gate, const void* w_up, const void* w_down,
+                      const void* routed, int routed_dtype, const int32_t* group_sizes,
+                      const int32_t* group_offsets, const int32_t* group_padded_offsets,
+                      const int32_t* group_idx_for_bx, void* out, int64_t P, int64_t H, int64_t I,
+                      int64_t E, int64_t V, int64_t nblk, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  return moe_run_prerouted_events(x, w_gate, w_up, w_down, routed, routed_dtype, group_sizes, group_offsets,
+                                  group_padded_offsets, group_idx_for_bx, out, P, H, I, E, V, nblk, workspace,
+                                  workspace_bytes, stream, nullptr);
 }
 
 int moe_route_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k,

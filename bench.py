@@ -172,30 +172,6 @@ def recorded_traffic(config, kernel_prefix):
     return None
 
 
-def stratified_tokens(ids, extra=8, seed=0, max_block_starts=64, block=128):
-    """Tokens whose rows cover the schedule of a routing: every touched
-    expert's first and last pair, up to ``max_block_starts`` block starts
-    (align order: by expert, then pair index) and ``extra`` random tokens."""
-    import numpy as np
-    ids = np.asarray(ids)
-    T, k = ids.shape
-    flat = ids.reshape(-1)
-    order = np.argsort(flat, kind="stable")
-    se = flat[order]
-    starts = np.flatnonzero(np.r_[True, se[1:] != se[:-1]])
-    ends = np.r_[starts[1:], flat.size]
-    rng = np.random.default_rng(seed)
-    pick, bstarts = set(), []
-    for a, b in zip(starts, ends):
-        pick.update((int(order[a]) // k, int(order[b - 1]) // k))
-        bstarts.extend(int(p) // k for p in order[a:b:block])
-    if len(bstarts) > max_block_starts:
-        bstarts = rng.choice(np.asarray(bstarts), max_block_starts, replace=False).tolist()
-    pick.update(bstarts)
-    pick.update(int(t) for t in rng.choice(T, min(extra, T), replace=False))
-    return np.asarray(sorted(pick), dtype=np.int64)
-
-
 def rb_group_sizes(E, valid, high, low_size):
     """remote_bench.py:60-75: E - high experts of low_size rows, the rest
     share the remainder, then interleaved (even positions first)."""
@@ -543,11 +519,11 @@ def main():
 
     check_res = None
     if not args.no_check:
-        from oracle import fused_moe_forward, route_topk, w8a8_forward
+        from oracle import fused_moe_forward, route_topk, stratified_tokens, w8a8_forward
         rid, _ = route_topk(inp["logits"].cpu().numpy(), k,
                             None if inp["bias"] is None else inp["bias"].cpu().numpy())
         ids_ok = bool(np.array_equal(ids_np, rid))
-        rows = stratified_tokens(rid)  # every expert's first / last pair, 64 block starts, 8 random
+        rows = stratified_tokens(rid, extra=8, max_block_starts=64)  # every expert's first / last pair
         r = torch.from_numpy(rows).to(dev)
         bias_c = None if inp["bias"] is None else inp["bias"].cpu()
         ref16 = fused_moe_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), inp["wg"], inp["wu"],

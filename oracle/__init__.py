@@ -41,6 +41,10 @@ Pinning (how each function is checked independently of its own formula):
                            gate (tests/test_oracle_fp8.py).
 * ``fused_moe_forward(shared=)`` -- exact doubling closed form and the dense
                            SwiGLU difference (tests/test_oracle_core.py).
+* ``stratified_tokens`` -- (a sampler, not arithmetic) every block of the
+                           routing's align holds a sampled token's pair, every
+                           expert's first and last pair is sampled
+                           (tests/test_oracle_align.py).
 """
 
 from .moe_ref import (  # noqa: F401
@@ -61,3 +65,4 @@ from .moe_ref import (  # noqa: F401
     w8a8_forward,
     silu_mul,
 )
+from .sampling import stratified_tokens  # noqa: F401

@@ -1,7 +1,7 @@
 """GPU parity of fused_moe (route -> align -> Stage1 -> Stage2 -> combine)
 against the CPU oracle, on every BASELINE config.  Every call writes into a
 NaN-poisoned output that must come back finite everywhere.  Full-size configs
-are checked on a stratified token set (tests/_cases.py stratified_tokens):
+are checked on a stratified token set (oracle/sampling.py stratified_tokens):
 the first and last pair of every touched expert and the first row of every
 block, so every item of both stages feeds a checked element; tokens are
 independent, so the oracle on those rows (with the full expert weights) is

@@ -4,7 +4,7 @@ invariants."""
 import numpy as np
 import pytest
 
-from oracle import align, metadata_from_group_sizes
+from oracle import align, metadata_from_group_sizes, route_topk
 
 
 def test_spec_example_metadata():
@@ -77,3 +77,32 @@ def test_align_capacity_bound(rng):
         al = align(ids, E, bm)
         P = T * k
         assert al["group_padded_offsets"][-1] <= P + min(E, P) * (bm - 1)
+
+
+def test_stratified_tokens_cover_every_block():
+    """The checkers' token sample holds, for every block of the align, a token
+    with a pair in that block, and every touched expert's first and last pair
+    (random dsv3-like routing, block sizes 128 and 256)."""
+    from oracle import stratified_tokens
+    rng = np.random.default_rng(3)
+    T, E, k = 1024, 64, 6
+    ids, _ = route_topk(rng.standard_normal((T, E)).astype(np.float32), k,
+                        (rng.standard_normal(E) * 0.8).astype(np.float32))
+    for bm in (128, 256):
+        rows = stratified_tokens(ids, block=bm, extra=0)
+        picked = np.zeros(T, bool)
+        picked[rows] = True
+        al = align(ids, E, bm)
+        sp, P = al["sorted_pair_ids"], T * k
+        for b in range(len(sp) // bm):
+            blk = sp[b * bm:(b + 1) * bm]
+            blk = blk[blk < P]
+            if blk.size:
+                assert picked[blk // k].any(), f"block {b} (bm={bm}) has no sampled token"
+        gs, go = al["group_sizes"], al["group_offsets"]
+        for e in range(E):
+            if gs[e]:
+                first = sp[al["group_padded_offsets"][e]]
+                last = sp[al["group_padded_offsets"][e] + gs[e] - 1]
+                assert picked[first // k] and picked[last // k]
+    assert len(stratified_tokens(ids, block=128, extra=0, max_block_starts=4)) < len(rows)

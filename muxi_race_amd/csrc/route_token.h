@@ -20,64 +20,111 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Order-preserving uint32 key of a float: larger float -> larger key; -0.0
+// keys as +0.0 (they compare equal) and NaN as 1, below every number.  Key 0
+// marks an expert past E.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) == 0) b = 0;
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 1u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key ^ 0x80000000u) : ~key);
+}
+
 // Routes token t from its logits v[j] = logit of expert l + 64 j (bias already
 // added; -inf where the expert is past E, `valid` bit j set otherwise).  Lane
 // j < k writes choice j to ids / wout at t * kout + j; with e_shared >= 0, lane
 // k appends the always-on shared expert (id e_shared, weight 1) as choice k
 // (kout = k + 1).
+//
+// Selection works on ballots and lane reads only, no cross-lane shuffles:
+//   1. tau = the k-th largest key, bit by bit from the top (a key prefix is
+//      kept when at least k keys reach it);
+//   2. the chosen set is every key > tau plus the lowest-numbered experts
+//      whose key equals tau, k in all;
+//   3. lanes 0..k-1 receive the chosen experts in ascending expert order, and
+//      each lane's choice index is the number of chosen keys above its own
+//      plus the equal keys of lower experts -- descending logit, ties to the
+//      lower expert;
+//   4. the softmax maximum is the key of choice 0; the probabilities of the k
+//      are renormalised over their sum taken in choice order.
 template <int VPL>
 __device__ __forceinline__ void route_token_values(const float (&v)[VPL], uint32_t valid, int t, int k,
                                                    int32_t* __restrict__ ids, float* __restrict__ wout,
                                                    int kout, int e_shared) {
   const int l = lane_id();
-  float m = -INFINITY;
+  uint32_t key[VPL];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j)
-    if (valid & (1u << j)) m = fmaxf(m, v[j]);
-  m = wave_max(m);
+  for (int j = 0; j < VPL; ++j) key[j] = (valid & (1u << j)) ? order_key(v[j]) : 0u;
+
+  uint32_t tau = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = tau | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    if (cnt >= k) tau = cand;
+  }
+
+  uint64_t sel[VPL];
+  int need = k;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    sel[j] = __ballot(key[j] > tau);
+    need -= __popcll(sel[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    uint64_t eq = __ballot(key[j] == tau);
+    while (need > 0 && eq) {
+      sel[j] |= eq & (~eq + 1);
+      eq &= eq - 1;
+      --need;
+    }
+  }
+
+  uint32_t mykey = 0;
+  int mye = 0, pos = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    uint64_t msk = sel[j];
+    while (msk) {
+      const int src = __ffsll((unsigned long long)msk) - 1;
+      msk &= msk - 1;
+      const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane((int)key[j], src);
+      if (l == pos) {
+        mykey = kk;
+        mye = src + 64 * j;
+      }
+      ++pos;
+    }
+  }
+  int rank = 0;
+  for (int q = 0; q < k; ++q) {
+    const uint32_t kq = (uint32_t)__builtin_amdgcn_readlane((int)mykey, q);
+    rank += (kq > mykey || (kq == mykey && q < l)) ? 1 : 0;
+  }
+  const bool chosen = l < k;
+
+  const int top = __ffsll((unsigned long long)__ballot(chosen && rank == 0)) - 1;
+  const float m = key_value((uint32_t)__builtin_amdgcn_readlane((int)mykey, top));
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j)
     if (valid & (1u << j)) s += expf(v[j] - m);
   s = wave_sum(s);
 
-  uint32_t taken = 0;
-  float my_p = 0.0f;
-  int my_id = 0;
+  const float pr = expf(key_value(mykey) - m) / s;
   float denom = 0.0f;
-  constexpr int kNone = 0x7fffffff;
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int be = kNone;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const uint32_t bit = 1u << j;
-      if ((valid & bit) && !(taken & bit) && (be == kNone || v[j] > bv)) {
-        bv = v[j];
-        be = l + 64 * j;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oe = __shfl_xor(be, o);
-      const bool take = oe != kNone && (be == kNone || ov > bv || (ov == bv && oe < be));
-      if (take) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    if ((be & 63) == l) taken |= 1u << (be >> 6);
-    const float pr = expf(bv - m) / s;
-    denom = denom + pr;  // selection order, identical in every lane
-    if (l == r) {
-      my_p = pr;
-      my_id = be;
-    }
+  for (int r = 0; r < k; ++r) {  // choice order, identical in every lane
+    const int src = __ffsll((unsigned long long)__ballot(chosen && rank == r)) - 1;
+    denom = denom + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), src));
   }
-  if (l < k) {
-    ids[(int64_t)t * kout + l] = my_id;
-    wout[(int64_t)t * kout + l] = my_p / denom;
+  if (chosen) {
+    ids[(int64_t)t * kout + rank] = mye;
+    wout[(int64_t)t * kout + rank] = pr / denom;
   } else if (l == k && e_shared >= 0) {
     ids[(int64_t)t * kout + k] = e_shared;
     wout[(int64_t)t * kout + k] = 1.0f;

@@ -186,6 +186,81 @@ __device__ __forceinline__ int bits_for(int E) {
   return nbits;
 }
 
+// Small batches (up to 64 * kAlignUnroll pairs per wave): the one-workgroup
+// kernel below with each wave's ids, ranks and group counts loaded once and
+// kept in registers from the count to the placement, rounds past the wave's
+// range skipped, and the padding written by all threads at once -- every used
+// row is first set to the sentinel P, then (after a barrier, which orders the
+// two writes of a row) the pairs overwrite their rows.  Same output as
+// align_kernel.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void align_small_kernel(
+    const int32_t* __restrict__ ids, int P, int E, int e_off, int BM, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ block_expert, int32_t* __restrict__ gs, int32_t* __restrict__ go,
+    int32_t* __restrict__ gpo) {
+  extern __shared__ int sm[];
+  int* hist = sm;                 // [NW][E]: wave w's count of expert e, then its first row among e's
+  int* tot = sm + NW * E;         // [E]
+  int* pstart = tot + E;          // [E+1] padded offsets
+  const int tid = threadIdx.x, w = tid >> 6, l = lane_id();
+  const int nbits = bits_for(E);
+  const int R = ((P + NW - 1) / NW + 63) / 64 * 64;  // <= 64 * kAlignUnroll (launch_align checks)
+  const int p0 = w * R, p1 = min(P, p0 + R);
+  const int nwa = R > 0 ? min(NW, (P + R - 1) / R) : 0;  // waves that hold pairs
+  int* hw = hist + w * E;
+  for (int i = l; i < E; i += 64) hw[i] = 0;
+  const uint64_t lt_mask = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  int ev[kAlignUnroll], rk[kAlignUnroll], cn[kAlignUnroll];
+#pragma unroll
+  for (int u = 0; u < kAlignUnroll; ++u) {
+    const int p = p0 + 64 * u + l;
+    ev[u] = p < p1 ? ids[p] : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < kAlignUnroll; ++u) {
+    rk[u] = 0;
+    cn[u] = 0;
+    if (p0 + 64 * u >= p1) {  // uniform: past the wave's range
+      ev[u] = -1;
+      continue;
+    }
+    const unsigned ue = (unsigned)ev[u] - (unsigned)e_off;
+    const bool ok = ue < (unsigned)E;
+    const int e = ok ? (int)ue : 0;
+    const uint64_t same = same_expert_mask(e, ok, nbits);
+    rk[u] = __popcll(same & lt_mask);
+    cn[u] = __popcll(same);
+    ev[u] = ok ? e : -1;
+    if (ok && rk[u] == 0) hw[e] += cn[u];
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 64 * NW) {
+    int run = 0;
+    for (int v = 0; v < nwa; ++v) {
+      const int c = hist[v * E + e];
+      hist[v * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (w == 0) align_expert_scan(tot, E, BM, pstart, true, gs, go, gpo);
+  __syncthreads();
+  const int rows = pstart[E];
+  for (int r = tid; r < rows; r += 64 * NW) sorted_ids[r] = P;
+  for (int e = tid; e < E; e += 64 * NW)
+    for (int b = pstart[e] / BM; b < pstart[e + 1] / BM; ++b) block_expert[b] = e;
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kAlignUnroll; ++u) {
+    const int e = ev[u];
+    if (e >= 0) {
+      sorted_ids[pstart[e] + hw[e] + rk[u]] = p0 + 64 * u + l;
+      if (rk[u] == 0) hw[e] += cn[u];
+    }
+  }
+}
+
 // One workgroup of NW waves; wave w owns the contiguous pair range
 // [w*R, (w+1)*R).  1. count into per-wave histograms; 2. per-wave exclusive
 // prefix per expert and the expert scan; 3. place; 4. fill.
@@ -304,12 +379,23 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
                         int32_t* whist, hipStream_t s, int e_off) {
   // 16 waves while the histograms fit 48 KiB of LDS, else 8 (E <= 1024)
   const bool w16 = 16 * E <= 12288;
+  const int nw = w16 ? 16 : 8;
+  const int per_wave = (P + nw - 1) / nw;  // pairs per wave in one workgroup
+  if (per_wave <= 64 * kAlignUnroll) {  // one workgroup, each wave's pairs held in registers
+    const size_t lds = sizeof(int) * (nw * (size_t)E + 2 * (size_t)E + 1);
+    if (w16)
+      hipLaunchKernelGGL(align_small_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, e_off, BM, sorted_ids,
+                         block_expert, gs, go, gpo);
+    else
+      hipLaunchKernelGGL(align_small_kernel<8>, dim3(1), dim3(512), lds, s, ids, P, E, e_off, BM, sorted_ids,
+                         block_expert, gs, go, gpo);
+    return hipGetLastError();
+  }
   const int G = align_groups(P);
   if (whist && G > 1) {
-    const int NW = w16 ? 16 : 8;
-    const int RW = align_pairs_per_group(P, G, NW);
-    const size_t lds1 = sizeof(int) * ((size_t)NW * E);
-    const size_t lds2 = sizeof(int) * ((size_t)NW * E + 3 * (size_t)E + 1);
+    const int RW = align_pairs_per_group(P, G, nw);
+    const size_t lds1 = sizeof(int) * ((size_t)nw * E);
+    const size_t lds2 = sizeof(int) * ((size_t)nw * E + 3 * (size_t)E + 1);
     if (w16) {
       hipLaunchKernelGGL(align_count_kernel<16>, dim3(G), dim3(1024), lds1, s, ids, P, E, e_off, RW, whist);
       hipLaunchKernelGGL(align_place_kernel<16>, dim3(G), dim3(1024), lds2, s, ids, P, E, e_off, BM, RW, whist,
@@ -321,15 +407,13 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
     }
     return hipGetLastError();
   }
-  if (w16) {
-    const size_t lds = sizeof(int) * (16 * (size_t)E + 2 * (size_t)E + 1);
+  const size_t lds = sizeof(int) * (nw * (size_t)E + 2 * (size_t)E + 1);
+  if (w16)
     hipLaunchKernelGGL(align_kernel<16>, dim3(1), dim3(1024), lds, s, ids, P, E, e_off, BM, sorted_ids,
                        block_expert, gs, go, gpo);
-  } else {
-    const size_t lds = sizeof(int) * (8 * (size_t)E + 2 * (size_t)E + 1);
+  else
     hipLaunchKernelGGL(align_kernel<8>, dim3(1), dim3(512), lds, s, ids, P, E, e_off, BM, sorted_ids,
                        block_expert, gs, go, gpo);
-  }
   return hipGetLastError();
 }
 

@@ -79,6 +79,29 @@ def test_align_edges():
     ids = np.stack([rng.choice(1024, 8, replace=False) for _ in range(5000)]).astype(np.int32)
     _align_both(ids, 1024, 32)                                     # many chunks, wide E (8 waves)
     _align_both(np.full((70000, 2), 7, np.int32), 16, 128)         # 64 workgroups, one hot expert
+    small = np.stack([rng.choice(1000, 8, replace=False) for _ in range(300)]).astype(np.int32)
+    _align_both(small, 1000, 32)                                   # small batch, wide E (8 waves)
+    _align_both(rng.integers(0, 256, (37, 7)).astype(np.int32), 256, 16)   # ragged small batch
+    _align_both(rng.integers(0, 8, (1024, 8)).astype(np.int32), 8, 128)    # 512 pairs per wave (limit)
+
+
+@pytest.mark.parametrize("T,k,E,bm", [(301, 3, 16, 64), (4000, 2, 16, 128)])
+def test_align_drops_out_of_range_ids(T, k, E, bm):
+    """Pairs whose id lies outside [0, E) are not placed.  Reference: the
+    oracle's align with those pairs sent to an extra last expert E, whose rows
+    come after every kept expert's and so leave theirs unchanged."""
+    from muxi_race_amd import moe_align
+    ids = np.random.default_rng(T).integers(-3, E + 3, (T, k)).astype(np.int32)
+    ref = align(np.where((ids >= 0) & (ids < E), ids, E).astype(np.int32), E + 1, bm)
+    got = moe_align(torch.from_numpy(ids).cuda(), E, bm)
+    torch.cuda.synchronize()
+    rows = int(ref["group_padded_offsets"][E])
+    assert int(got["group_padded_offsets"][E]) == rows
+    np.testing.assert_array_equal(got["sorted_pair_ids"][:rows].cpu().numpy(), ref["sorted_pair_ids"][:rows])
+    np.testing.assert_array_equal(got["block_expert"][:rows // bm].cpu().numpy(), ref["block_expert"][:rows // bm])
+    np.testing.assert_array_equal(got["group_sizes"].cpu().numpy(), ref["group_sizes"][:E])
+    np.testing.assert_array_equal(got["group_offsets"].cpu().numpy()[:E], ref["group_offsets"][:E])
+    np.testing.assert_array_equal(got["group_padded_offsets"].cpu().numpy(), ref["group_padded_offsets"][:E + 1])
 
 
 def test_align_many_workgroups_matches_one_on_dropped_ids():

@@ -124,8 +124,8 @@ def test_fp8_workspace_sized_for_128_rows_keeps_128_row_padding():
     assert_close(b, a, atol=1e-3, rtol=1e-3, what="128-row padding vs 256")
 
 
-def test_fp8_w8a8_config_sampled():
-    _run(moe_inputs("w8a8", 72), sample="strat")
+def test_fp8_w8a8_config_full():
+    _run(moe_inputs("w8a8", 72))
 
 
 def test_fp8_decode():

@@ -375,7 +375,7 @@ def probe_ring(dev, reps=5):
     shapes = {0: (384, "384 rows (128 + 256 or 256 + 128), 3 stages, 8 waves", 1024),
               2: (96, "96 rows (32 + 64), 6 stages, 4 waves", 2048)}
     cases = [(0, 14336, h) for h in (0, 128, 256, 320, 384)] + [(0, 4096, h) for h in (0, 128, 256, 320, 384)] + \
-            [(1, 14336, 0), (1, 14336, 128), (1, 4096, 0), (1, 4096, 128),
+            [(1, 14336, h) for h in (0, 128, 256, 320)] + [(1, 4096, h) for h in (0, 128, 256, 320)] + [
              (2, 14336, 0), (3, 14336, 0), (2, 4096, 0), (3, 4096, 0)]
     need = max(shapes[v & 2][2] * shapes[v & 2][0] * p for v, p, _ in cases)
     buf = torch.zeros(need, dtype=torch.uint8, device=dev)

@@ -118,3 +118,25 @@ def test_align_many_workgroups_matches_one_on_dropped_ids():
     assert torch.equal(a["block_expert"][:rows // 64], b["block_expert"][:rows // 64])
     for key in ("group_sizes", "group_offsets", "group_padded_offsets"):
         assert torch.equal(a[key], b[key])
+
+
+def test_routing_signed_zero_and_nan_order():
+    """-0.0 and +0.0 are equal logits (ties to the lower expert), and a NaN
+    logit ranks below every number, as in the oracle's stable sort of -v.
+    Ids only: a NaN in the row makes the oracle's softmax NaN."""
+    from muxi_race_amd import route_topk as gpu_route
+    E, k = 70, 6
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn((64, E), generator=g)
+    logits[0] = 0.0
+    logits[0, ::2] = -0.0                      # alternating signed zeros: experts 0..5
+    logits[1, :] = -1.0
+    logits[1, [3, 9, 40]] = float("nan")       # NaNs never beat -1
+    logits[2, :8] = float("nan")               # NaN in the first 8 experts: after every number
+    logits[3, : E - 2] = float("nan")          # only 2 numbers: they come first, then NaNs by index
+    ids, _ = gpu_route(logits.cuda(), k, None)
+    torch.cuda.synchronize()
+    rid, _ = route_topk(logits.numpy(), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rid)
+    np.testing.assert_array_equal(ids[0].cpu().numpy(), np.arange(k))
+    np.testing.assert_array_equal(ids[3, :2].cpu().numpy(), [E - 2, E - 1])

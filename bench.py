@@ -373,18 +373,20 @@ def probe_ring(dev, reps=5):
     # (variant, rows, ring, workgroups): 1 workgroup per CU for the 144 KiB
     # ring, 2 for the 72 KiB one; 4 rounds of the chip either way
     shapes = {0: (384, "384 rows (128 + 256 or 256 + 128), 3 stages, 8 waves", 1024),
-              2: (96, "96 rows (32 + 64), 6 stages, 4 waves", 2048)}
+              2: (96, "96 rows (32 + 64), 6 stages, 4 waves", 2048),
+              4: (512, "512 rows (256 + 256), 2 stages, 8 waves", 1024)}
     cases = [(0, 14336, h) for h in (0, 128, 256, 320, 384)] + [(0, 4096, h) for h in (0, 128, 256, 320, 384)] + \
             [(1, 14336, h) for h in (0, 128, 256, 320)] + [(1, 4096, h) for h in (0, 128, 256, 320)] + [
-             (2, 14336, 0), (3, 14336, 0), (2, 4096, 0), (3, 4096, 0)]
-    need = max(shapes[v & 2][2] * shapes[v & 2][0] * p for v, p, _ in cases)
+             (2, 14336, 0), (3, 14336, 0), (2, 4096, 0), (3, 4096, 0)] + \
+            [(4, p, h) for p in (14336, 4096) for h in (0, 256)]
+    need = max(shapes[v & 6][2] * shapes[v & 6][0] * p for v, p, _ in cases)
     buf = torch.zeros(need, dtype=torch.uint8, device=dev)
-    hit = torch.zeros(384 * 14336, dtype=torch.uint8, device=dev)
+    hit = torch.zeros(512 * 14336, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4096, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     out = []
     for v, pitch, hr in cases:
-        rows, shape, groups = shapes[v & 2]
+        rows, shape, groups = shapes[v & 6]
         nk = pitch // 128
         call = lambda: fn(v, buf.data_ptr(), need, hit.data_ptr(), hit.numel(), pitch, nk, hr, groups,
                           sink.data_ptr(), stream)

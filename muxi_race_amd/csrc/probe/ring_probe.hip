@@ -52,15 +52,16 @@ __global__ __launch_bounds__(64 * NW) void ring_probe_kernel(const char* __restr
 
 // variant: 0 / 1 = 384-row stages (the 128-row kernels' 128 + 256 or 256 + 128
 // rows), 8 waves, 3 stages, default / non-temporal streamed rows; 2 / 3 =
-// 96-row stages (the 32-row decode kernels' shape), 4 waves, 6 stages.
+// 96-row stages (the 32-row decode kernels' shape), 4 waves, 6 stages; 4 / 5 =
+// 512-row stages (256 + 256 rows), 8 waves, 2 stages.
 // stream_bytes / hit_bytes: sizes of the two regions (groups * rows * pitch
 // and hit_rows * pitch at least); sink holds `groups` ints.  Returns 0, -1 for
 // bad arguments (nothing launched), or the HIP error.
 extern "C" int moe_probe_ring(int variant, const void* stream_base, int64_t stream_bytes, const void* hit_base,
                               int64_t hit_bytes, int64_t pitch, int nk, int hit_rows, int groups, int* sink,
                               void* stream) {
-  const int rows = variant < 2 ? 384 : 96;
-  if (variant < 0 || variant > 3 || !stream_base || !sink || groups <= 0 || nk <= 0 || pitch % 16 != 0 ||
+  const int rows = variant < 2 ? 384 : (variant < 4 ? 96 : 512);
+  if (variant < 0 || variant > 5 || !stream_base || !sink || groups <= 0 || nk <= 0 || pitch % 16 != 0 ||
       (int64_t)nk * moe::kRowBytes > pitch || hit_rows < 0 || hit_rows > rows || hit_rows % 8 != 0 ||
       (int64_t)groups * rows * pitch > stream_bytes || (hit_rows > 0 && (!hit_base || (int64_t)hit_rows * pitch > hit_bytes)))
     return -1;
@@ -71,7 +72,9 @@ extern "C" int moe_probe_ring(int variant, const void* stream_base, int64_t stre
     case 0: hipLaunchKernelGGL((moe::ring_probe_kernel<384, 8, 3, false>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
     case 1: hipLaunchKernelGGL((moe::ring_probe_kernel<384, 8, 3, true>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
     case 2: hipLaunchKernelGGL((moe::ring_probe_kernel<96, 4, 6, false>), dim3(groups), dim3(256), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
-    default: hipLaunchKernelGGL((moe::ring_probe_kernel<96, 4, 6, true>), dim3(groups), dim3(256), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
+    case 3: hipLaunchKernelGGL((moe::ring_probe_kernel<96, 4, 6, true>), dim3(groups), dim3(256), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
+    case 4: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, false>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
+    default: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, true>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
   }
   return (int)hipGetLastError();
 }

@@ -595,11 +595,21 @@ def main():
             ref8 = w8a8_forward(inp["x"][r].cpu(), inp["logits"][r].cpu(), codes(qw.q_gate),
                                 qw.s_gate.cpu().numpy(), codes(qw.q_up), qw.s_up.cpu().numpy(),
                                 codes(qw.q_down), qw.s_down.cpu().numpy(), k, bias_c, fmt=fmt).float()
-            check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
-                         f"{fmt}_oracle_within_rtol2e-2_atol1e-2": tol(ref8),
+            check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows)}
+            if fmt == "fp8":
+                # the fp8 gate of the tests: where the GPU's fp32 sum and the oracle's exact one
+                # straddle an e4m3 rounding boundary an intermediate code moves one step, so a
+                # few elements leave the fp16 gate; relative L2 <= 1e-2 and >= 99.9% inside it
+                rel8 = float((got - ref8).norm() / ref8.norm())
+                in8 = float(((got - ref8).abs() <= 1e-2 + 2e-2 * ref8.abs()).float().mean())
+                check_res.update({"fp8_oracle_rel_l2": round(rel8, 6), "fp8_oracle_frac_in_fp16_gate": round(in8, 6),
+                                  "fp8_oracle_gate_met": bool(torch.isfinite(got).all()) and rel8 <= 1e-2 and in8 >= 0.999})
+            else:
+                check_res[f"{fmt}_oracle_within_rtol2e-2_atol1e-2"] = tol(ref8)
+            check_res.update({
                          "rel_l2_vs_fp16_oracle": round(float((got - ref16).norm() / ref16.norm()), 5),
                          "frac_within_atol1e-2_rtol5e-2_vs_fp16_oracle":
-                             round(float(((got - ref16).abs() <= 1e-2 + 5e-2 * ref16.abs()).float().mean()), 4)}
+                             round(float(((got - ref16).abs() <= 1e-2 + 5e-2 * ref16.abs()).float().mean()), 4)})
         else:
             check_res = {"routing_ids_bit_exact": ids_ok, "sampled_tokens": len(rows),
                          "within_rtol2e-2_atol1e-2": tol(ref16)}

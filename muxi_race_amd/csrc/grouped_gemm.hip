@@ -324,10 +324,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
             const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
-            uint32_t packed = 0;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) packed |= quant_code<F8>(hv[b][a][4 * rg + q], inv) << (8 * q);
-            *reinterpret_cast<uint32_t*>(hrow + n) = packed;
+            *reinterpret_cast<uint32_t*>(hrow + n) =
+                quant_code4<F8>(hv[b][a][4 * rg], hv[b][a][4 * rg + 1], hv[b][a][4 * rg + 2], hv[b][a][4 * rg + 3], inv);
           }
         // scales are stored block-major: [I/128][hs_stride]
         if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = hscale;

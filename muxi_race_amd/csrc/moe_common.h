@@ -235,35 +235,37 @@ __device__ __forceinline__ int quant_i8(float x, float inv) {
 }
 
 // OCP fp8 e4m3 code of v, round to nearest even, saturating at +-448 (the
-// callers scale so that |v| <= 448).  Normals: the fp32 mantissa is rounded to
-// 3 bits with the carry running into the exponent, which is rebiased 127 -> 7;
-// below 2^-6 the code is the multiple of 2^-9 (rint is round-to-even).
+// callers scale so that |v| <= 448): the gfx950 conversion instruction
+// (v_cvt_pk_fp8_f32, two codes per instruction) on v clamped to [-448, 448].
+// Its codes equal a bit-level restatement of the format -- the fp32 mantissa
+// rounded to 3 bits with the carry running into the rebiased exponent, and
+// below 2^-6 the round-to-even multiple of 2^-9 -- for every float of
+// magnitude <= 448 (the load-path probe library's moe_probe_f8_encoder,
+// run by the fp8 GPU tests).
+__device__ __forceinline__ float f8_clamp(float v) { return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f); }
 __device__ __forceinline__ uint32_t f8_e4m3(float v) {
-  const uint32_t u = __float_as_uint(v);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const float a = __builtin_fabsf(v);
-  uint32_t code;
-  if (a >= 0.015625f) {
-    const uint32_t au = __float_as_uint(a);
-    code = ((au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20) - (120u << 3);
-    code = code > 0x7Eu ? 0x7Eu : code;
-  } else {
-    code = (uint32_t)__builtin_rintf(a * 512.0f);
-  }
-  return sign | code;
+  const float c = f8_clamp(v);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, c, 0, false) & 0xffu;
+}
+// codes of a, b, c, d in bytes 0..3
+__device__ __forceinline__ uint32_t f8_e4m3x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(f8_clamp(a), f8_clamp(b), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(f8_clamp(c), f8_clamp(d), lo, true);
 }
 
 // Largest code magnitude of the 8-bit formats: int8 (symmetric) and fp8 e4m3.
 template <bool F8> constexpr float qmax() { return F8 ? 448.0f : 127.0f; }
 
-// 8-bit code (low byte) of x * inv: int8 round-half-away or fp8 e4m3.
+// 8-bit codes (int8 round-half-away or fp8 e4m3) of x[0..3] * inv packed
+// into bytes 0..3.
 template <bool F8>
-__device__ __forceinline__ uint32_t quant_code(float x, float inv) {
-  if constexpr (F8) {
+__device__ __forceinline__ uint32_t quant_code4(float x0, float x1, float x2, float x3, float inv) {
 #pragma clang fp contract(off)
-    return f8_e4m3(x * inv);
+  if constexpr (F8) {
+    return f8_e4m3x4(x0 * inv, x1 * inv, x2 * inv, x3 * inv);
   } else {
-    return (uint32_t)quant_i8(x, inv) & 0xffu;
+    return ((uint32_t)quant_i8(x0, inv) & 0xffu) | (((uint32_t)quant_i8(x1, inv) & 0xffu) << 8) |
+           (((uint32_t)quant_i8(x2, inv) & 0xffu) << 16) | (((uint32_t)quant_i8(x3, inv) & 0xffu) << 24);
   }
 }
 

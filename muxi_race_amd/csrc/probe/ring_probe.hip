@@ -1,4 +1,5 @@
-// Load-path probe (measurement only; not part of the operator library): it
+// Load-path probe and encoder check (measurement and verification only; not
+// part of the operator library).  The load-path probe
 // streams tile rows through the same direct-to-LDS ring as the GEMM stages --
 // DmaTile's global_load_lds_dwordx4 with the row swizzle, wait_stages,
 // barrier_no_fence -- and does no compute, so its rate is the ceiling the
@@ -76,5 +77,66 @@ extern "C" int moe_probe_ring(int variant, const void* stream_base, int64_t stre
     case 4: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, false>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
     default: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, true>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
   }
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fp8 encoder check: the library's f8_e4m3 (the gfx950 conversion
+// instruction) against a bit-level restatement of OCP e4m3 with round to
+// nearest even, for every float of magnitude <= 448.  Normals (>= 2^-6): the
+// fp32 mantissa rounded to 3 bits (add 0x7FFFF plus the kept lsb, drop 20
+// bits), the carry running into the exponent, rebiased from 127 to 7;
+// subnormals: the round-to-even multiple of 2^-9.
+// ---------------------------------------------------------------------------
+namespace moe {
+__device__ __forceinline__ uint32_t f8_e4m3_bits(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = __builtin_fabsf(v);
+  uint32_t code;
+  if (a >= 0.015625f) {
+    const uint32_t au = __float_as_uint(a);
+    code = ((au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20) - (120u << 3);
+    code = code > 0x7Eu ? 0x7Eu : code;
+  } else {
+    code = (uint32_t)__builtin_rintf(a * 512.0f);
+  }
+  return sign | code;
+}
+
+// thread t checks the 256 bit patterns [256 t, 256 t + 256); 2^24 threads
+__global__ __launch_bounds__(256) void f8_check_kernel(unsigned long long* __restrict__ mismatches,
+                                                        unsigned long long* __restrict__ compared) {
+  const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  unsigned long long bad = 0, seen = 0;
+  for (uint32_t i = 0; i < 256; i += 4) {
+    float v[4];
+    bool in[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = __uint_as_float((uint32_t)(t * 256 + i + j));
+      in[j] = __builtin_fabsf(v[j]) <= 448.0f;  // false for NaN
+    }
+    const uint32_t packed = f8_e4m3x4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!in[j]) continue;
+      ++seen;
+      const uint32_t ref = f8_e4m3_bits(v[j]);
+      if (f8_e4m3(v[j]) != ref || ((packed >> (8 * j)) & 0xffu) != ref) ++bad;
+    }
+  }
+  atomicAdd(compared, seen);
+  if (bad) atomicAdd(mismatches, bad);
+}
+}  // namespace moe
+
+// Counts, over every float of magnitude <= 448 (2 * (0x43E00000 + 1) of
+// them), the values whose code from f8_e4m3 or from the packed f8_e4m3x4
+// differs from the bit-level restatement.  Both counters are added to (the
+// caller zeroes them).  Returns 0 or the HIP error.
+extern "C" int moe_probe_f8_encoder(unsigned long long* mismatches, unsigned long long* compared, void* stream) {
+  if (!mismatches || !compared) return -1;
+  hipLaunchKernelGGL(moe::f8_check_kernel, dim3(1u << 16), dim3(256), 0, (hipStream_t)stream, mismatches, compared);
   return (int)hipGetLastError();
 }

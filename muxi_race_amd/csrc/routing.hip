@@ -474,10 +474,8 @@ hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void*
 // ---------------------------------------------------------------------------
 template <bool F8>
 __device__ __forceinline__ u32x2 quant_pack8(f16x8 v, float inv) {
-  u32x2 packed = {0u, 0u};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) packed[i >> 2] |= quant_code<F8>((float)v[i], inv) << (8 * (i & 3));
-  return packed;
+  return u32x2{quant_code4<F8>((float)v[0], (float)v[1], (float)v[2], (float)v[3], inv),
+               quant_code4<F8>((float)v[4], (float)v[5], (float)v[6], (float)v[7], inv)};
 }
 
 template <int NCH, bool F8>

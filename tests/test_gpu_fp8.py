@@ -146,6 +146,25 @@ def test_fp8_dsv3_sampled():
     _run(inp, sample="strat", experts=top, extra=8)
 
 
+def test_fp8_encoder_matches_the_format_for_every_float():
+    """The kernels' e4m3 encoder (the gfx950 conversion instruction, one and
+    four codes at a time) against a bit-level restatement of the format with
+    round to nearest even, over every float of magnitude <= 448 -- all the
+    values the quantisers feed it (libmoe_probe.so's moe_probe_f8_encoder)."""
+    import ctypes
+    from pathlib import Path
+    path = Path(__file__).resolve().parents[1] / "muxi_race_amd" / "libmoe_probe.so"
+    fn = ctypes.CDLL(str(path)).moe_probe_f8_encoder
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    cnt = torch.zeros(2, dtype=torch.int64, device="cuda")
+    assert fn(cnt.data_ptr(), cnt.data_ptr() + 8, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    bad, seen = (int(v) for v in cnt.cpu())
+    assert seen == 2 * (0x43E00000 + 1), seen
+    assert bad == 0, f"{bad} floats encode differently"
+
+
 def test_fp8_is_deterministic():
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     inp = moe_inputs("small", 75, T=256)

@@ -374,11 +374,13 @@ def probe_ring(dev, reps=5):
     # ring, 2 for the 72 KiB one; 4 rounds of the chip either way
     shapes = {0: (384, "384 rows (128 + 256 or 256 + 128), 3 stages, 8 waves", 1024),
               2: (96, "96 rows (32 + 64), 6 stages, 4 waves", 2048),
-              4: (512, "512 rows (256 + 256), 2 stages, 8 waves", 1024)}
+              4: (512, "512 rows (256 + 256), 2 stages, 8 waves", 1024),
+              6: (384, "384 rows, 3 stages, 8 waves; hit rows issued by waves 0-3, streamed rows by 4-7", 1024)}
     cases = [(0, 14336, h) for h in (0, 128, 256, 320, 384)] + [(0, 4096, h) for h in (0, 128, 256, 320, 384)] + \
             [(1, 14336, h) for h in (0, 128, 256, 320)] + [(1, 4096, h) for h in (0, 128, 256, 320)] + [
              (2, 14336, 0), (3, 14336, 0), (2, 4096, 0), (3, 4096, 0)] + \
-            [(4, p, h) for p in (14336, 4096) for h in (0, 256)]
+            [(4, p, h) for p in (14336, 4096) for h in (0, 256)] + \
+            [(v, p, h) for p in (14336, 4096) for v, h in ((6, 128), (7, 256))]
     need = max(shapes[v & 6][2] * shapes[v & 6][0] * p for v, p, _ in cases)
     buf = torch.zeros(need, dtype=torch.uint8, device=dev)
     hit = torch.zeros(512 * 14336, dtype=torch.uint8, device=dev)
@@ -403,7 +405,7 @@ def probe_ring(dev, reps=5):
         torch.cuda.synchronize()
         sec = a.elapsed_time(b) / reps * 1e-3
         step_bytes = groups * nk * 128
-        out.append(dict(ring=shape, row_pitch=pitch, hit_rows=hr, policy="non-temporal" if v & 1 else "default",
+        out.append(dict(ring=shape, row_pitch=pitch, hit_rows=hr, policy="non-temporal" if v & 1 and v < 6 else "default",
                         us=round(sec * 1e6, 1), streamed_tb_per_s=round(step_bytes * (rows - hr) / sec / 1e12, 2),
                         lds_fill_tb_per_s=round(step_bytes * rows / sec / 1e12, 2)))
         print(f"probe {out[-1]}", file=sys.stderr, flush=True)

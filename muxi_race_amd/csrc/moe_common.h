@@ -92,8 +92,8 @@ __device__ __forceinline__ void barrier_no_fence() {
 // decode-sized (32-row) kernels.  A weight tile read by exactly one item is
 // loaded non-temporal (the gfx950 `nt` bit, cache-policy immediate 2):
 // measured with the load-path probe (csrc/probe/ring_probe.hip, the 96-row
-// decode ring), streaming reads rise from 6.24 to 7.07 TB/s (rows 14 KiB
-// apart) and from 5.59 to 6.19 TB/s (4 KiB apart), and decode from 0.575 to
+// decode ring), streaming reads rise from 6.15 to 7.12 TB/s (rows 14 KiB
+// apart) and from 5.45 to 6.14 TB/s (4 KiB apart), and decode from 0.575 to
 // 0.533 ms.  Weight tiles that sibling items of a multi-block
 // expert re-read from L2, and token / intermediate rows, keep the default
 // policy (non-temporal there measured slower: fewer L2 hits); the wide-tile

@@ -49,20 +49,76 @@ __global__ __launch_bounds__(64 * NW) void ring_probe_kernel(const char* __restr
   if (threadIdx.x == 0) sink[blockIdx.x] = *reinterpret_cast<const int*>(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE);
 }
 
+
+// As ring_probe_kernel (384 rows, 8 waves, 3 stages), with the hit rows and
+// the streamed rows issued by different waves: waves 0..3 load the first HIT
+// tile rows (the shared region), waves 4..7 the other 384 - HIT rows, each
+// group in the DmaTile layout of its own rows.  A wave's loads retire in
+// order; here no wave holds hits queued behind misses.
+template <int HIT>
+__global__ __launch_bounds__(512) void ring_probe_split_kernel(const char* __restrict__ stream_base,
+                                                                const char* __restrict__ hit_base, int64_t pitch,
+                                                                int nk, int* __restrict__ sink) {
+  constexpr int ROWS = 384, NW = 8, S = 3, TW = 4;
+  constexpr int QT = HIT / (8 * TW), QW = (ROWS - HIT) / (8 * (NW - TW));
+  static_assert(QT * 8 * TW == HIT && QW * 8 * (NW - TW) == ROWS - HIT, "row groups per wave");
+  constexpr int STAGE = ROWS * kRowBytes;
+  __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
+  const int w = wave_id(), l = lane_id();
+  const bool tok = w < TW;
+  const int wr = tok ? w : w - TW;   // wave index within its group
+  const int nw = tok ? TW : NW - TW; // waves of its group
+  const int q = tok ? QT : QW;
+  const char* own = stream_base + (int64_t)blockIdx.x * ROWS * pitch;
+  const char* src[QW > QT ? QW : QT];
+  int dst[QW > QT ? QW : QT];
+#pragma unroll
+  for (int i = 0; i < (QW > QT ? QW : QT); ++i) {
+    const int g = (tok ? 0 : HIT / 8) + nw * i + wr;  // row group (8 rows, 1 KiB of LDS)
+    const int r = 8 * g + (l >> 3);
+    src[i] = (tok ? hit_base : own) + (int64_t)r * pitch + (((l & 7) ^ swz(r)) << 4);
+    dst[i] = 1024 * g;
+  }
+  auto issue = [&](int buf, int k) {
+#pragma unroll
+    for (int i = 0; i < (QW > QT ? QW : QT); ++i)
+      if (i < q) dma_to_lds<16>(src[i] + (size_t)k * kRowBytes, smem + buf * STAGE + dst[i]);
+  };
+  auto wait = [&](int ahead) {
+    if (tok) wait_stages<QT, S - 2>(ahead);
+    else wait_stages<QW, S - 2>(ahead);
+  };
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s, s);
+  int cur = 0;
+  for (int k = 0; k < nk; ++k) {
+    wait(nk - 1 - k);
+    barrier_no_fence();
+    if (k + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, k + S - 1);
+    cur = cur + 1 == S ? 0 : cur + 1;
+  }
+  wait_vmcnt<0>();
+  barrier_no_fence();
+  if (threadIdx.x == 0) sink[blockIdx.x] = *reinterpret_cast<const int*>(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE);
+}
 }  // namespace moe
 
 // variant: 0 / 1 = 384-row stages (the 128-row kernels' 128 + 256 or 256 + 128
 // rows), 8 waves, 3 stages, default / non-temporal streamed rows; 2 / 3 =
 // 96-row stages (the 32-row decode kernels' shape), 4 waves, 6 stages; 4 / 5 =
-// 512-row stages (256 + 256 rows), 8 waves, 2 stages.
+// 512-row stages (256 + 256 rows), 8 waves, 2 stages; 6 / 7 = the 384-row ring
+// with hit rows and streamed rows issued by different waves (ring_probe_split_kernel),
+// hit_rows 128 / 256 (fixed by the variant).
 // stream_bytes / hit_bytes: sizes of the two regions (groups * rows * pitch
 // and hit_rows * pitch at least); sink holds `groups` ints.  Returns 0, -1 for
 // bad arguments (nothing launched), or the HIP error.
 extern "C" int moe_probe_ring(int variant, const void* stream_base, int64_t stream_bytes, const void* hit_base,
                               int64_t hit_bytes, int64_t pitch, int nk, int hit_rows, int groups, int* sink,
                               void* stream) {
-  const int rows = variant < 2 ? 384 : (variant < 4 ? 96 : 512);
-  if (variant < 0 || variant > 5 || !stream_base || !sink || groups <= 0 || nk <= 0 || pitch % 16 != 0 ||
+  const int rows = variant < 2 || variant > 5 ? 384 : (variant < 4 ? 96 : 512);
+  if (variant == 6 || variant == 7) hit_rows = variant == 6 ? 128 : 256;
+  if (variant < 0 || variant > 7 || !stream_base || !sink || groups <= 0 || nk <= 0 || pitch % 16 != 0 ||
       (int64_t)nk * moe::kRowBytes > pitch || hit_rows < 0 || hit_rows > rows || hit_rows % 8 != 0 ||
       (int64_t)groups * rows * pitch > stream_bytes || (hit_rows > 0 && (!hit_base || (int64_t)hit_rows * pitch > hit_bytes)))
     return -1;
@@ -75,7 +131,9 @@ extern "C" int moe_probe_ring(int variant, const void* stream_base, int64_t stre
     case 2: hipLaunchKernelGGL((moe::ring_probe_kernel<96, 4, 6, false>), dim3(groups), dim3(256), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
     case 3: hipLaunchKernelGGL((moe::ring_probe_kernel<96, 4, 6, true>), dim3(groups), dim3(256), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
     case 4: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, false>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
-    default: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, true>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
+    case 5: hipLaunchKernelGGL((moe::ring_probe_kernel<512, 8, 2, true>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, hit_rows, sink); break;
+    case 6: hipLaunchKernelGGL((moe::ring_probe_split_kernel<128>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, sink); break;
+    default: hipLaunchKernelGGL((moe::ring_probe_split_kernel<256>), dim3(groups), dim3(512), 0, s, sb, hb, pitch, nk, sink); break;
   }
   return (int)hipGetLastError();
 }

@@ -137,7 +137,7 @@ def test_probe_library_rejects_bad_arguments_without_gpu():
                    ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     buf = ctypes.create_string_buffer(64)
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert fn(7, p, 1 << 40, p, 1 << 40, 4096, 32, 0, 1, p, None) == -1          # no such variant
+    assert fn(99, p, 1 << 40, p, 1 << 40, 4096, 32, 0, 1, p, None) == -1         # no such variant
     assert fn(0, p, 1 << 40, p, 1 << 40, 4096, 33, 0, 1, p, None) == -1          # K past the row
     assert fn(0, p, 1 << 40, p, 1 << 40, 4096, 32, 12, 1, p, None) == -1         # hit rows not a multiple of 8
     assert fn(0, p, 1000, p, 1 << 40, 4096, 32, 0, 1, p, None) == -1             # stream region too small

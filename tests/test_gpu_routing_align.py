@@ -38,7 +38,7 @@ def test_routing_bit_exact(name):
     np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
 
 
-@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (256, 8), (1000, 32), (3, 3)])
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (256, 8), (1000, 32), (3, 3), (1, 1), (8, 8), (5, 1), (65, 32)])
 def test_routing_ties(E, k):
     g = torch.Generator().manual_seed(E)
     logits = (torch.randn((257, E), generator=g) * 2).round() / 2  # many exact ties

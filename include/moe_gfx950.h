@@ -270,9 +270,12 @@ int moe_fused_forward_shard(const void* x, const float* logits, const float* bia
  * q = 0, scale = 0.  Weights [E, N, K] are quantised as R = E*N rows.
  *
  * moe_fused_forward_w8a8: as moe_fused_forward with int8 weights + fp32
- * per-row scales; activations are quantised per token inside the call, the
- * SiLU*up intermediate per (row, 128 columns), and the GEMMs run on i8 MFMA
- * with int32 accumulation and fused dequantisation.
+ * per-row scales; activations are quantised per token inside the call, and
+ * so is the SiLU*up intermediate (computed in fp32 from the dequantised gate /
+ * up products, rounded to fp16, then one int8 scale per routed row); both
+ * GEMMs run on i8 MFMA with int32 accumulation over the whole of K and the
+ * dequantisation fused into their epilogues.  Workspace
+ * moe_fused_workspace_bytes(..., w8a8 = 1).
  * ---------------------------------------------------------------------- */
 int moe_quantize_rows_w8(const void* w, int64_t R, int64_t K, int8_t* q, float* scale,
                          void* stream);
@@ -295,12 +298,13 @@ int moe_fused_forward_w8a8_events(const void* x, const float* logits, const floa
                                   void* const* stage_events);
 
 /* ------------------------------------------------------------------------
- * FP8 (OCP e4m3) variant of the W8A8 path: the same pipeline and scale layout
- * with e4m3 codes in place of int8 and fp32 accumulation on the gfx950 f8 MFMA
+ * FP8 (OCP e4m3) variant of the W8A8 path: the same pipeline with e4m3 codes
+ * in place of int8 and fp32 accumulation on the gfx950 f8 MFMA
  * (v_mfma_f32_32x32x64_f8f6f4).  moe_quantize_rows_fp8: per-row scale =
  * max|row|/448, code = e4m3(w * (448/max|row|)) rounded to nearest even; all-
- * zero rows give code 0 and scale 0.  Activations are quantised per token and
- * the SiLU*up intermediate per (row, 128 columns) the same way, inside the call.
+ * zero rows give code 0 and scale 0.  Activations are quantised per token the
+ * same way inside the call; the SiLU*up intermediate per (row, 128 columns)
+ * with power-of-two scales, which the scaled f8 MFMA applies.
  * moe_fused_forward_fp8 takes stage_events as moe_fused_forward_events (or
  * NULL); workspace moe_fused_workspace_bytes(..., w8a8 = 2) (one sized for
  * block_m = 128 also works, without the 256-row padding).  Extends the

@@ -37,12 +37,16 @@ int64_t cap_rows(int64_t T, int64_t k, int64_t E, int64_t bm) {
 }
 
 struct FusedLayout {
-  int64_t ids, w, sorted, bexp, gs, go, gpo, whist, h, hs, xq, sx, ypair, total;
+  int64_t ids, w, sorted, bexp, gs, go, gpo, whist, h, hq, hs, xq, sx, ypair, total;
 };
 
+// qt: moe::kQF16, kQI8 or kQF8.  The intermediate h is fp16 for fp16 and int8
+// operands (int8 quantises it per row afterwards, into hq + hs), fp8 codes
+// for fp8 (with per-(row, 128-column) scales in hs).
 FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int64_t bm,
-                         bool w8) {
+                         int qt) {
   FusedLayout L{};
+  const bool w8 = qt != moe::kQF16, i8 = qt == moe::kQI8;
   const int64_t P = T * k, rows = cap_rows(T, k, E, bm);
   int64_t o = 0;
   L.ids = o; o += up(P * 4);
@@ -53,8 +57,9 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, 
   L.go = o; o += up((E + 1) * 4);
   L.gpo = o; o += up((E + 1) * 4);
   L.whist = o; o += up((int64_t)moe::align_groups((int)P) * E * 4);  // align workgroup histograms
-  L.h = o; o += up(rows * I * (w8 ? 1 : 2));
-  L.hs = o; o += w8 ? up(rows * (I / moe::kBN) * 4) : 0;  // [I/128][rows], block-major
+  L.h = o; o += up(rows * I * (qt == moe::kQF8 ? 1 : 2));
+  L.hq = o; o += i8 ? up(rows * I) : 0;                   // int8: per-row codes of h
+  L.hs = o; o += w8 ? up(rows * (i8 ? 1 : I / moe::kBN) * 4) : 0;  // int8 [rows]; fp8 [I/128][rows], block-major
   L.xq = o; o += w8 ? up(T * H) : 0;
   L.sx = o; o += w8 ? up(T * 4) : 0;
   L.ypair = o; o += up(P * H * 2);
@@ -253,9 +258,10 @@ int64_t moe_pick_block_m(int64_t T, int64_t E, int64_t k) { return pick_bm(T, E,
 int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
                                   int64_t block_m, int w8a8) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
-  // w8a8: 0 fp16, nonzero 8-bit (1 int8, 2 fp8: one padding rule for both)
+  // w8a8: 0 fp16, 1 int8, 2 fp8 (one padding rule for all)
+  if (w8a8 < 0 || w8a8 > 2) return 0;
   block_m = align_bm(T, E, k, H, block_m);
-  return fused_layout(T, H, I, E, k, block_m, w8a8 != 0).total;
+  return fused_layout(T, H, I, E, k, block_m, w8a8 == 2 ? moe::kQF8 : (w8a8 ? moe::kQI8 : moe::kQF16)).total;
 }
 
 // The always-on shared expert (wg_s / wu_s / wd_s non-null, fp16 only) runs as
@@ -306,15 +312,15 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
     return fail(MOE_ERR_INVALID_ARG, "x, weights, scales, out and workspace must be 16-byte aligned");
   const int64_t router_ws = w_router ? moe_router_workspace_bytes(T, H, E) : 0;
   // a workspace sized for the 128-row padding (block_m = 128) keeps it
-  if (block_m == 256 && workspace_bytes < fused_layout(T, H, I, Ee, ke, 256, w8).total + router_ws) block_m = 128;
-  const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, w8);
+  if (block_m == 256 && workspace_bytes < fused_layout(T, H, I, Ee, ke, 256, qt).total + router_ws) block_m = 128;
+  const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, qt);
   const int64_t need = L.total + router_ws;
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
   // rows per item of each stage: block_m, except that over the 256-row
-  // padding Stage 2 keeps 128-row (paired) items for fp16 and int8 (fp8
-  // takes 256-row ones; see align_bm)
+  // padding Stage 2 keeps 128-row (paired) items for fp16 (the 8-bit formats
+  // take 256-row ones; see align_bm)
   const int64_t bm1 = block_m;
-  const int64_t bm2 = block_m == 256 && qt == moe::kQF8 ? 256 : (block_m == 256 ? 128 : block_m);
+  const int64_t bm2 = block_m == 256 && qt == moe::kQF16 ? 128 : block_m;
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);
@@ -346,7 +352,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p1.wg = (const char*)wg;
   p1.wu = (const char*)wu;
   p1.h = ws + L.h;
-  p1.h_scale = w8 ? (float*)(ws + L.hs) : nullptr;
+  p1.h_scale = qt == moe::kQF8 ? (float*)(ws + L.hs) : nullptr;
   p1.hs_stride = rows;
   p1.x_scale = w8 ? (const float*)(ws + L.sx) : nullptr;
   p1.sg = sg;
@@ -364,10 +370,16 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p1.H = H;
   p1.I = I;
   if ((rc = check_launch(moe::launch_stage1(p1, (int)bm1, qt, true, rows / bm1, s), "stage1"))) return rc;
+  // int8: h (fp16) -> per-row int8 codes + scales, for the routed rows only
+  // (sorted id below the sentinel T * ke, row below gpo[E])
+  if (qt == moe::kQI8 &&
+      (rc = check_launch(moe::launch_quant_rows(ws + L.h, rows, I, ws + L.hq, (float*)(ws + L.hs), moe::kQI8, s,
+                                                sorted, (int32_t)(T * ke), gpo + Ee), "quantize_h")))
+    return rc;
   mark(4);
 
   moe::Stage2Params p2{};
-  p2.a = ws + L.h;
+  p2.a = qt == moe::kQI8 ? ws + L.hq : ws + L.h;
   p2.a_scale = w8 ? (const float*)(ws + L.hs) : nullptr;
   p2.as_stride = rows;
   p2.wd = (const char*)wd;
@@ -425,7 +437,7 @@ int64_t moe_fused_shared_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_
                                          int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   block_m = align_bm(T, E + 1, k + 1, H, block_m);
-  return fused_layout(T, H, I, E + 1, k + 1, block_m, false).total + moe_router_workspace_bytes(T, H, E);
+  return fused_layout(T, H, I, E + 1, k + 1, block_m, moe::kQF16).total + moe_router_workspace_bytes(T, H, E);
 }
 
 int moe_fused_forward_shared(const void* x, const float* logits, const void* w_router, const float* bias,
@@ -446,7 +458,7 @@ int64_t moe_fused_ex_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   const int64_t s = shared ? 1 : 0;
   block_m = align_bm(T, E + s, k + s, H, block_m);
-  return fused_layout(T, H, I, E + s, k + s, block_m, false).total + (with_router ? moe_router_workspace_bytes(T, H, E) : 0);
+  return fused_layout(T, H, I, E + s, k + s, block_m, moe::kQF16).total + (with_router ? moe_router_workspace_bytes(T, H, E) : 0);
 }
 
 int moe_fused_forward_ex(const void* x, const float* logits, const void* w_router, const float* bias,
@@ -467,7 +479,7 @@ int64_t moe_fused_shard_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t
                                         int64_t E_local, int64_t block_m) {
   if (T < 0 || H <= 0 || I <= 0 || E_total <= 0 || E_local <= 0 || k <= 0) return 0;
   block_m = align_bm(T, E_total, k, H, block_m);
-  return fused_layout(T, H, I, E_local, k, block_m, false).total;
+  return fused_layout(T, H, I, E_local, k, block_m, moe::kQF16).total;
 }
 
 int moe_fused_forward_shard(const void* x, const float* logits, const float* bias, const void* w_gate,
@@ -535,8 +547,8 @@ int moe_fused_forward_noalloc(const void* x, const float* logits, const float* b
   if (T == 0) return MOE_OK;
   // the padding the call will use: 256-row blocks only where they fit (as
   // for any workspace sized for 128-row blocks)
-  int64_t need = fused_layout(T, H, I, E, k, bm, false).total;
-  if (bm == 256 && need > kNoAllocScratchBytes) need = fused_layout(T, H, I, E, k, 128, false).total;
+  int64_t need = fused_layout(T, H, I, E, k, bm, moe::kQF16).total;
+  if (bm == 256 && need > kNoAllocScratchBytes) need = fused_layout(T, H, I, E, k, 128, moe::kQF16).total;
   if (need > kNoAllocScratchBytes)
     return fail(MOE_ERR_WORKSPACE,
                 "moe_fused_forward_noalloc: T=%lld H=%lld I=%lld E=%lld k=%lld needs %lld bytes of scratch, the "

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using LD = DmaTile<ROWS, NW>;
   constexpr int STAGE = ROWS * kRowBytes;
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
-  static_assert(!(PAIR && I8), "int8 quantises h per 128-column tile: items must span 128 columns");
+  static_assert(!(PAIR && F8), "fp8 quantises h per 128-column tile: items must span 128 columns");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
 
@@ -241,8 +241,11 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   __syncthreads();  // every wave is done with the ring before LDS is reused
 
   const int l = lane_id();
-  if constexpr (!I8) {
+  if constexpr (!F8) {
     // h = silu(g) * u -> fp16, valid rows only (submission.py:1532-1542).
+    // int8: g and u dequantised first, (acc * s_x[token]) * s_w[e, n]; the
+    // intermediate is quantised per row afterwards (quant_rows_kernel), so
+    // Stage 2 accumulates in int32 over the whole of K.
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
       const int m = xr0 + 32 * b + (l & 31);
@@ -254,18 +257,34 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int rg = 0; rg < 4; ++rg) {
             const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
             f16x4 v;
+            if constexpr (I8) {
+              f32x4 gs, us;
+              if constexpr (kHoistFeat) {
+                gs = sgv[a][rg];
+                us = suv[a][rg];
+              } else {
+                gs = *reinterpret_cast<const f32x4*>(sgrow + n);
+                us = *reinterpret_cast<const f32x4*>(surow + n);
+              }
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              v[q] = (_Float16)silu_mul(ag[a][b][4 * rg + q], au[a][b][4 * rg + q]);
+              for (int q = 0; q < 4; ++q) {
+                const float g = ((float)ag[a][b][4 * rg + q] * sxv[b]) * gs[q];
+                const float u = ((float)au[a][b][4 * rg + q] * sxv[b]) * us[q];
+                v[q] = (_Float16)silu_mul(g, u);
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                v[q] = (_Float16)silu_mul(ag[a][b][4 * rg + q], au[a][b][4 * rg + q]);
+            }
             *reinterpret_cast<f16x4*>(hrow + n) = v;
           }
       }
     }
   } else {
-    // Dequantise (acc * s_x[token]) * s_w[e, n], h = silu(g) * u, then quantise
-    // h per (row, this 128-column tile) to the operands' 8-bit format: amax
-    // over the tile's columns, which are spread over the lane pair (l, l^32)
-    // and the WAVES_N waves.
+    // fp8: dequantise (acc * s_x[token]) * s_w[e, n], h = silu(g) * u, then quantise
+    // h per (row, this 128-column tile) to e4m3: amax over the tile's columns,
+    // which are spread over the lane pair (l, l^32) and the WAVES_N waves.
     float* red = reinterpret_cast<float*>(smem);  // [WAVES_N][BM]; loop ended with a barrier
     float hv[L::NBM][L::NBN][16];
 #pragma unroll
@@ -305,17 +324,11 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < L::WAVES_N; ++j) amax = fmaxf(amax, red[j * BM + mrow]);
-      // int8: scale amax/127.  fp8: the power-of-two scale 2^j (amax <= 448 * 2^j),
-      // which Stage 2's f8 MFMA applies itself; dividing by it is exact.
-      float inv, hscale;
-      if constexpr (F8) {
-        const int sb = pow2_scale_e8m0(amax);
-        hscale = amax > 0.0f ? scale_from_e8m0(sb) : 0.0f;
-        inv = amax > 0.0f ? scale_from_e8m0(254 - sb) : 0.0f;  // 2^-j (sb = 0: 2^127, the exact inverse of 2^-127)
-      } else {
-        inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
-        hscale = amax / qmax<F8>();
-      }
+      // The power-of-two scale 2^j (amax <= 448 * 2^j), which Stage 2's f8
+      // MFMA applies itself; dividing by it is exact.
+      const int sb = pow2_scale_e8m0(amax);
+      const float hscale = amax > 0.0f ? scale_from_e8m0(sb) : 0.0f;
+      const float inv = amax > 0.0f ? scale_from_e8m0(254 - sb) : 0.0f;  // 2^-j (sb = 0: 2^127, the exact inverse of 2^-127)
       if (mrow < actual) {
         const int64_t grow = row0 + mrow;
         int8_t* hrow = reinterpret_cast<int8_t*>(p.h) + grow * p.h_ld;
@@ -325,7 +338,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int rg = 0; rg < 4; ++rg) {
             const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
             *reinterpret_cast<uint32_t*>(hrow + n) =
-                quant_code4<F8>(hv[b][a][4 * rg], hv[b][a][4 * rg + 1], hv[b][a][4 * rg + 2], hv[b][a][4 * rg + 3], inv);
+                quant_code4<true>(hv[b][a][4 * rg], hv[b][a][4 * rg + 1], hv[b][a][4 * rg + 2], hv[b][a][4 * rg + 3], inv);
           }
         // scales are stored block-major: [I/128][hs_stride]
         if (wn == 0 && l < 32) p.h_scale[(int64_t)(n0 / kBN) * p.hs_stride + grow] = hscale;
@@ -467,10 +480,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   constexpr bool I8 = QT != kQF16;  // 8-bit operands (int8 or fp8) with row / block scales
   constexpr bool F8 = QT == kQF8;
   using L = Layout<BM, WAVES_M, BN, NW>;
+  // int8: exact int32 accumulation over the whole of K (the intermediate has
+  // one scale per row, applied in the epilogue); fp16 / fp8: fp32
+  using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + BN;
   using LD = DmaTile<ROWS, NW>;
-  constexpr int SCALES = ROWS * kRowBytes;                // 8-bit: row scales of the step
-  constexpr int STAGE = SCALES + (I8 ? 256 * NW : 0);
+  constexpr int SCALES = ROWS * kRowBytes;                // fp8: row scales of the step
+  constexpr int STAGE = SCALES + (F8 ? 256 * NW : 0);
   static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
   __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
@@ -536,6 +552,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // are never stored.)
   int64_t orow[L::NBM];
   float wr[L::NBM];
+  float shv[L::NBM];  // int8: the intermediate's row scale (0 for padding rows)
   if constexpr (FUSED) {
     int pid[L::NBM];
 #pragma unroll
@@ -545,6 +562,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       const bool valid = xr0 + 32 * b + (l & 31) < actual;
       orow[b] = valid ? pid[b] : 0;
       wr[b] = reinterpret_cast<const float*>(p.routed)[valid ? pid[b] : 0];
+      if constexpr (I8 && !F8) shv[b] = valid ? p.a_scale[row0 + xr0 + 32 * b + (l & 31)] : 0.0f;
     }
   } else {
 #pragma unroll
@@ -562,26 +580,26 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
                              : reinterpret_cast<const float*>(p.routed)[ridx];
     }
   }
-  f32x16 acc[L::NBN][L::NBM];
+  Acc acc[L::NBN][L::NBM];
 #pragma unroll
   for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
-    for (int b = 0; b < L::NBM; ++b) acc[a][b] = f32x16{};
+    for (int b = 0; b < L::NBM; ++b) acc[a][b] = Acc{};
 
-  // int8: the row scales of K step ks (block-major layout, so contiguous) ride
+  // fp8: the row scales of K step ks (block-major layout, so contiguous) ride
   // in the same stage: wave w loads rows 64w..64w+63 (clamped inside the tile)
   // with one dword DMA, so every wave issues the same number of loads.
   const float* scale_src = nullptr;
-  if constexpr (I8) {
+  if constexpr (F8) {
     const int r = 64 * wave_id() + l;
     scale_src = p.a_scale + row0 + (r < actual ? r : 0);
   }
-  constexpr int Q = LD::NI + (I8 ? 1 : 0);
+  constexpr int Q = LD::NI + (F8 ? 1 : 0);
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
     if constexpr (STREAM) ld.issue(st, k, w.shared ? kNoStream : rx);
     else ld.issue(st, k);
-    if constexpr (I8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
+    if constexpr (F8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
   // K loop instantiated per count of live token blocks (see Stage 1).
   auto main_loop = [&](auto nb_c) {
@@ -604,7 +622,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(st, wr0 + 32 * a, s);
         };
-        if constexpr (!I8) {
+        if constexpr (!F8) {
+          // fp16 (fp32 accumulation) or int8 (int32 accumulation)
           load_frags(0, 0);
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
@@ -617,54 +636,27 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
               for (int b = 0; b < NB; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
           }
         } else {
-          // One K step of 8-bit operands is one 128-column scale block of the
+          // One K step of fp8 operands is one 128-column scale block of the
           // intermediate, with one scale per token row.
           const float* scl = reinterpret_cast<const float*>(st + SCALES);
           float sc[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) sc[b] = scl[xr0 + 32 * b + (l & 31)];
-          if constexpr (F8) {
-            // fp8: the row scales are powers of two, applied by the MFMA itself
-            // (E8M0 exponent byte of each token row's scale), straight into acc
-            int sb[NB];
+          // The row scales are powers of two, applied by the MFMA itself
+          // (E8M0 exponent byte of each token row's scale), straight into acc.
+          int sb[NB];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) sb[b] = (int)(__float_as_uint(sc[b]) >> 23);
+          for (int b = 0; b < NB; ++b) sb[b] = (int)(__float_as_uint(sc[b]) >> 23);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              load_frags(0, 2 * j);
-              load_frags(1, 2 * j + 1);
-              __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-              for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-                  acc[a][b] = mma8_scale_b(wf[0][a], wf[1][a], af[0][b], af[1][b], acc[a][b], sb[b]);
-            }
-          } else {
-            // int8: exact int32 partial product of the step, then
-            // acc += partial * s_h[row, block]
-            i32x16 ia[L::NBN][NB];
-#pragma unroll
-            for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-              for (int b = 0; b < NB; ++b) ia[a][b] = i32x16{};
-            load_frags(0, 0);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const int fb = s & 1;
-              if (s < 3) load_frags(fb ^ 1, s + 1);
-              __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-              for (int a = 0; a < L::NBN; ++a)
-#pragma unroll
-                for (int b = 0; b < NB; ++b) ia[a][b] = mma(wf[fb][a], af[fb][b], ia[a][b]);
-            }
+          for (int j = 0; j < 2; ++j) {
+            load_frags(0, 2 * j);
+            load_frags(1, 2 * j + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
               for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][b][r] += (float)ia[a][b][r] * sc[b];
+                acc[a][b] = mma8_scale_b(wf[0][a], wf[1][a], af[0][b], af[1][b], acc[a][b], sb[b]);
           }
         }
       }
@@ -688,7 +680,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
         f16x4 v;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          float y = acc[a][b][4 * rg + q];
+          float y = (float)acc[a][b][4 * rg + q];
+          if constexpr (I8 && !F8) y = y * shv[b];  // int8: ((acc * s_h[row]) * s_d[n]) * w
           if constexpr (I8) y = y * sd[q];
           // select, never multiply, so NaN/Inf garbage in padding rows cannot leak
           v[q] = valid ? (_Float16)(y * wr[b]) : (_Float16)0.0f;
@@ -812,7 +805,7 @@ hipError_t launch_stage1(const Stage1Params& params, int block_m, int qt, bool g
       if (qt == kQF8) return go1<64, 1, 4, kQF8, true, false>(p, grid, s);
       return go1<64, 1, 4, kQF16, true, false>(p, grid, s);
     case 128:
-      if (qt == kQI8) return go1<128, 2, NW, kQI8, true, false>(p, grid, s);
+      if (qt == kQI8) return go1<128, 2, NW, kQI8, true, kPair>(p, grid, s);
       if (qt == kQF8) return go1<128, 2, NW, kQF8, true, false>(p, grid, s);
       return go1<128, 2, NW, kQF16, true, kPair>(p, grid, s);
     case 256:
@@ -850,8 +843,9 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, int qt, bool f
       if (qt == kQF8) return go2_128<kQF8, true>(p, mb, s);
       return go2_128<kQF16, true>(p, mb, s);
     case 256:
-      // fp8, 256 token rows x 256 weight rows: two 64 KiB stages
+      // 8-bit, 256 token rows x 256 weight rows: two 64 KiB stages
       if (qt == kQF8 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQF8, true, false>(p, mb, s);
+      if (qt == kQI8 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQI8, true, false>(p, mb, s);
       return hipErrorInvalidValue;
   }
   return hipErrorInvalidValue;

@@ -16,12 +16,12 @@ struct Stage1Params {
   const char* x;            // fp16 [rows, H] (direct) / fp16|int8 [T, H] (gather)
   const char* wg;           // [E, I, H]
   const char* wu;           // [E, I, H]
-  char* h;                  // fp16|int8 [padded rows, I]
-  float* h_scale;           // int8 only: [I/128][hs_stride] (block-major)
-  int64_t hs_stride;        // int8 only: rows of each h_scale block (>= padded rows)
-  const float* x_scale;     // int8 only: [T]
-  const float* sg;          // int8 only: [E, I]
-  const float* su;          // int8 only: [E, I]
+  char* h;                  // fp16 [padded rows, I] (fp16 and int8 operands) | fp8 [padded rows, I]
+  float* h_scale;           // fp8 only: [I/128][hs_stride] (block-major)
+  int64_t hs_stride;        // fp8 only: rows of each h_scale block (>= padded rows)
+  const float* x_scale;     // 8-bit only: [T]
+  const float* sg;          // 8-bit only: [E, I]
+  const float* su;          // 8-bit only: [E, I]
   const int32_t* gs;        // [E]
   const int32_t* gpo;       // [E+1]
   const int32_t* sorted_ids;  // gather only: [padded rows], sentinel = T*topk
@@ -42,11 +42,11 @@ struct Stage1Params {
 
 // Stage 2: y = h Wd^T, scaled by the routing weight of each row.
 struct Stage2Params {
-  const char* a;            // fp16|int8 [padded rows, I]
-  const float* a_scale;     // int8 only: [I/128][as_stride] (block-major)
-  int64_t as_stride;        // int8 only: rows of each a_scale block (>= padded rows)
+  const char* a;            // fp16|int8|fp8 [padded rows, I]
+  const float* a_scale;     // int8: [padded rows] (per row); fp8: [I/128][as_stride] (block-major)
+  int64_t as_stride;        // fp8 only: rows of each a_scale block (>= padded rows)
   const char* wd;           // [E, H, I]
-  const float* sd;          // int8 only: [E, H]
+  const float* sd;          // 8-bit only: [E, H]
   char* out;                // pre-routed: fp16 [P, H]; fused: fp16 [T*topk, H]
   const void* routed;       // pre-routed: [V] raw order (fp32|fp16); fused: fp32 [T*topk]
   int routed_f16;
@@ -109,8 +109,11 @@ hipError_t launch_router(const void* x, const void* w_router, const float* bias,
 hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream, const int32_t* ids = nullptr, int e_lo = 0, int e_n = 0);
 // Per-row 8-bit quantisation of an fp16 [R, K] matrix to the format qt
-// (kQI8 or kQF8): codes into q, amax / qmax into scale.
+// (kQI8 or kQF8): codes into q, amax / qmax into scale.  With `ids` set only
+// rows r < *used_rows (a device value) with ids[r] < sentinel are quantised
+// (the int8 intermediate: rows in the expert-sorted space).
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,
-                             hipStream_t stream);
+                             hipStream_t stream, const int32_t* ids = nullptr, int32_t sentinel = 0,
+                             const int32_t* used_rows = nullptr);
 
 }  // namespace moe

@@ -478,13 +478,21 @@ __device__ __forceinline__ u32x2 quant_pack8(f16x8 v, float inv) {
                quant_code4<F8>((float)v[4], (float)v[5], (float)v[6], (float)v[7], inv)};
 }
 
+//
+// With `ids` set, row r is quantised only if r < *used_rows and ids[r] <
+// sentinel: the intermediate's rows in the expert-sorted space, where rows
+// past the experts' padded range and padding rows (sentinel id) are never
+// written by Stage 1 and are left alone here.
 template <int NCH, bool F8>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ w, int64_t R,
                                                          int64_t K, uint8_t* __restrict__ q,
-                                                         float* __restrict__ scale) {
+                                                         float* __restrict__ scale,
+                                                         const int32_t* __restrict__ ids, int32_t sentinel,
+                                                         const int32_t* __restrict__ used_rows) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int l = lane_id();
   if (r >= R) return;
+  if (ids && (r >= *used_rows || ids[r] >= sentinel)) return;
   const _Float16* row = w + r * K;
   uint8_t* qrow = q + r * K;
   float amax = 0.0f;
@@ -521,7 +529,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
 }
 
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,
-                             hipStream_t s) {
+                             hipStream_t s, const int32_t* ids, int32_t sentinel, const int32_t* used_rows) {
   if (R == 0) return hipSuccess;
   const dim3 grid((unsigned)((R + 3) / 4)), block(256);
   const _Float16* src = reinterpret_cast<const _Float16*>(w);
@@ -530,9 +538,9 @@ hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float
 #define MOE_QR(N)                                                                               \
   do {                                                                                          \
     if (qt == kQF8)                                                                             \
-      hipLaunchKernelGGL((quant_rows_kernel<N, true>), grid, block, 0, s, src, R, K, dst, scale);  \
+      hipLaunchKernelGGL((quant_rows_kernel<N, true>), grid, block, 0, s, src, R, K, dst, scale, ids, sentinel, used_rows);  \
     else                                                                                        \
-      hipLaunchKernelGGL((quant_rows_kernel<N, false>), grid, block, 0, s, src, R, K, dst, scale); \
+      hipLaunchKernelGGL((quant_rows_kernel<N, false>), grid, block, 0, s, src, R, K, dst, scale, ids, sentinel, used_rows); \
   } while (0)
   if (nch <= 4) MOE_QR(4);
   else if (nch <= 8) MOE_QR(8);

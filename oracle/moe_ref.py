@@ -393,15 +393,21 @@ def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k
     """W8A8 fused MoE on the CPU (the GPU path's arithmetic contract).
 
     x rows are quantised per token; gate/up are exact 8-bit GEMMs dequantised
-    as (acc * s_x[t]) * s_w[e, n]; h = silu(g) * u is quantised per (row,
-    ``scale_block`` columns); the down GEMM accumulates each column block's
-    exact product times its row scale, in block order, then applies
-    s_down[e, n] and the routing weight; pairs are combined in choice order.
-    fmt "int8": int8 codes (wq_* int8); "fp8": OCP e4m3 codes (wq_* uint8),
-    whose products are exact in float64 (8 significant bits each, sums of at
-    most 2**14 terms between 2**-18 and 2**18); the GPU sums them in fp32.  The
-    fp8 intermediate takes power-of-two scales (``pow2_scales``), which the
-    GPU's f8 MFMA applies itself.
+    as (acc * s_x[t]) * s_w[e, n]; h = silu(g) * u.  Pairs are combined in
+    choice order.
+
+    fmt "int8" (wq_* int8): h is rounded to fp16 and quantised per row, like
+    x (one scale per routed row, over all I columns); the down GEMM is one
+    exact integer product over the whole of K, dequantised as
+    ((acc * s_h[row]) * s_down[e, n]) * routing weight.
+
+    fmt "fp8" (wq_* uint8, OCP e4m3 codes, whose products are exact in
+    float64: 8 significant bits each, sums of at most 2**14 terms between
+    2**-18 and 2**18; the GPU sums them in fp32): h is quantised per (row,
+    ``scale_block`` columns) with power-of-two scales (``pow2_scales``), which
+    the GPU's f8 MFMA applies itself; the down GEMM accumulates each column
+    block's exact product times its row scale, in block order, then applies
+    s_down[e, n] and the routing weight.
     """
     if fmt == "fp8":
         quant = quantize_rows_fp8
@@ -434,15 +440,18 @@ def w8a8_forward(x, logits, wq_gate, s_gate, wq_up, s_up, wq_down, s_down, top_k
         u = (_exact_matmul(a, val(wq_up[e])).astype(np.float32) * sx[tok][:, None]).astype(np.float32)
         u = (u * s_up[e][None, :]).astype(np.float32)
         h = silu_mul(torch.from_numpy(g), torch.from_numpy(u)).numpy().astype(np.float32)
-        nb = I // scale_block
-        hb = h.reshape(n, nb, scale_block)
-        hq, sh = quantize_rows_fp8(hb, pow2=True) if fmt == "fp8" else quant(hb)  # [n, nb, 128], [n, nb]
-        hq = val(hq)
         wd = val(wq_down[e])
-        acc = np.zeros((n, H), dtype=np.float32)
-        for b in range(nb):
-            part = _exact_matmul(hq[:, b, :], wd[:, b * scale_block:(b + 1) * scale_block])
-            acc = (acc + part.astype(np.float32) * sh[:, b : b + 1]).astype(np.float32)
+        if fmt == "fp8":
+            nb = I // scale_block
+            hq, sh = quantize_rows_fp8(h.reshape(n, nb, scale_block), pow2=True)  # [n, nb, 128], [n, nb]
+            hq = val(hq)
+            acc = np.zeros((n, H), dtype=np.float32)
+            for b in range(nb):
+                part = _exact_matmul(hq[:, b, :], wd[:, b * scale_block:(b + 1) * scale_block])
+                acc = (acc + part.astype(np.float32) * sh[:, b : b + 1]).astype(np.float32)
+        else:
+            hq, sh = quantize_rows_int8(h.astype(np.float16))  # [n, I], [n]
+            acc = (_exact_matmul(hq, wd).astype(np.float32) * sh[:, None]).astype(np.float32)
         y = (acc * s_down[e][None, :]).astype(np.float32)
         y = (y * wflat[pairs][:, None]).astype(np.float32)
         y_pair[pairs] = y

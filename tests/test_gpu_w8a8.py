@@ -3,12 +3,13 @@ against the W8A8 oracle (same quantised arithmetic) and within the north-star
 gate (relative L2 <= 5e-2) against the fp16 oracle.
 
 Elementwise against the fp16 oracle the W8A8 path is reported, not gated at
-100%: per-row weight and per-token activation int8 at H = 7168 leave ~2.4%
-relative L2, and about 13% of elements fall outside |d| <= 1e-2 + 5e-2 |ref|
-(a property of the quantisation scheme, the same for the oracle's own W8A8
-arithmetic).  The fraction inside is printed and held above 0.80.
-Full-size outputs are NaN-poisoned and must come back finite; the w8a8
-config's whole output is compared."""
+100%: per-row weight int8 and per-token int8 of both activations (x and the
+SiLU*up intermediate) at H = 7168, I = 2048 leave ~3% relative L2, and about
+a quarter of the elements fall outside |d| <= 1e-2 + 5e-2 |ref| (a property of
+the quantisation scheme, the same for the oracle's own W8A8 arithmetic: 0.76
+inside on a T = 128, E = 8 slice of these dimensions).  The fraction inside
+is printed and held above 0.70.  Full-size outputs are NaN-poisoned and must
+come back finite; the w8a8 config's whole output is compared."""
 import numpy as np
 import pytest
 import torch
@@ -19,7 +20,7 @@ from oracle import fused_moe_forward, quantize_rows_int8, route_topk, w8a8_forwa
 
 pytestmark = pytest.mark.gpu
 W8A8_REL_L2 = 5e-2
-W8A8_ELEMENTWISE_FLOOR = 0.80  # fraction within 1e-2 + 5e-2 |ref| of the fp16 oracle
+W8A8_ELEMENTWISE_FLOOR = 0.70  # fraction within 1e-2 + 5e-2 |ref| of the fp16 oracle
 
 
 @pytest.mark.parametrize("K", [1024, 2048 + 8, 7168, 8200])  # register path (4, 8, 16 chunks) and two-pass
@@ -75,10 +76,12 @@ def test_w8a8_small(bm):
     _run(moe_inputs("small", 21), block_m=bm)
 
 
-def test_w8a8_skewed_ragged():
-    """int8 over the 256-row padding (Stage 1 on 256-row items, Stage 2 on
-    128-row ones): an empty expert, partial and multi-block experts."""
-    _run(skewed_8bit_case(22))
+@pytest.mark.parametrize("bm", [0, 128])
+def test_w8a8_skewed_ragged(bm):
+    """An empty expert, partial and multi-block experts, over the library's
+    256-row padding (both stages on 256-row items) and over 128-row blocks
+    (Stage 1 pairs the blocks of multi-block experts, Stage 2 too)."""
+    _run(skewed_8bit_case(22), block_m=bm)
 
 
 def test_w8a8_config_full():
@@ -88,8 +91,10 @@ def test_w8a8_config_full():
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
 def test_intermediate_scale_blocks(fmt):
     """I = 256 with h's second 128-column block ~1000x its first (the oracle's
-    scale-contrast case): the GPU keeps the small block (per-block scales) and
-    matches the 8-bit oracle elementwise."""
+    scale-contrast case), against the 8-bit oracle elementwise.  int8 takes
+    one scale per row: the small block's codes are 0 and out[:, 0] (which
+    reads only that block) is exactly 0.  fp8 takes per-(row, 128-column)
+    scales and keeps the small block."""
     from muxi_race_amd import fused_moe, quantize_w8a8_weights
     from oracle import quantize_rows_fp8
     qfn = quantize_rows_int8 if fmt == "int8" else quantize_rows_fp8
@@ -101,5 +106,27 @@ def test_intermediate_scale_blocks(fmt):
     ref8 = w8a8_forward(x, lg, codes(qw.q_gate), qw.s_gate.cpu().numpy(), codes(qw.q_up), qw.s_up.cpu().numpy(),
                         codes(qw.q_down), qw.s_down.cpu().numpy(), k, fmt=fmt).float()
     assert_close(out, ref8, what=f"{fmt} scale contrast vs oracle")
-    rel0 = float((out[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
-    assert rel0 < (5e-2 if fmt == "int8" else 8e-2), rel0
+    if fmt == "int8":
+        assert float(out[:, 0].abs().max()) == 0.0
+    else:
+        rel0 = float((out[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
+        assert rel0 < 8e-2, rel0
+
+
+def test_int8_invariant_under_intermediate_permutation():
+    """int32 accumulation over the whole of K and one intermediate scale per
+    row: permuting the I columns (gate/up rows and w_down columns alike, across
+    128-column blocks) leaves the int8 output bit-identical."""
+    from muxi_race_amd import fused_moe, quantize_w8a8_weights
+    inp = moe_inputs("small", 23)
+    I = inp["I"]
+    perm = torch.randperm(I, generator=torch.Generator().manual_seed(23)).cuda()
+    outs = []
+    for p in (None, perm):
+        wg, wu, wd = inp["wg"], inp["wu"], inp["wd"]
+        if p is not None:
+            wg, wu, wd = wg[:, p].contiguous(), wu[:, p].contiguous(), wd[:, :, p].contiguous()
+        qw = quantize_w8a8_weights(wg, wu, wd)
+        outs.append(fused_moe(inp["x"], inp["logits"], None, None, None, inp["k"], expert_bias=inp["bias"], w8a8=qw))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(outs[0]).all()) and torch.equal(outs[0], outs[1])

@@ -68,8 +68,7 @@ def test_w8a8_against_fp16_oracle():
 
 def test_w8a8_exact_on_representable_inputs():
     """Inputs already on the int8 grid (x and weights = integer * 2^-n with a
-    row maximum of 127 steps) quantise losslessly, so gate/up are exact; with
-    I = 128 the intermediate has one scale block per row."""
+    row maximum of 127 steps) quantise losslessly, so gate/up are exact."""
     rng = np.random.default_rng(3)
     T, H, I, E, k = 8, 128, 128, 2, 1
     xi = rng.integers(-127, 128, size=(T, H)).astype(np.float32)
@@ -91,25 +90,62 @@ def test_w8a8_exact_on_representable_inputs():
     out = w8a8_forward(x, lg, qg, sg, qg, sg, qd, sd, k).float()
     ref = fused_moe_forward(x, lg, wg, wg, wd, k).float()
     # only the intermediate requantisation remains (h = silu(g)*g is heavy
-    # tailed, ~1.3% here): error well under the gate
+    # tailed, ~1.3% here, plus h's fp16 rounding): error well under the gate
     assert float((out - ref).norm() / ref.norm()) < 2e-2
 
 
-def test_w8a8_intermediate_scale_is_per_128_columns():
-    """Per-(row, 128-column) intermediate scales keep the small block: out[:, 0]
-    stays within 5% of the fp16 oracle.  One scale per row would quantise the
-    small block (|h| < amax / 254) to 0 and give out[:, 0] = 0 exactly; taking
-    the scales in the wrong block order would multiply it by ~1000."""
+def test_w8a8_int8_intermediate_scale_is_per_row():
+    """int8 quantises h with one scale per routed row.  In the scale-contrast
+    case (I = 256, h's second 128-column block ~1000x its first) the small
+    block's codes are all 0 (|h| < amax / 254), so out[:, 0], which reads only
+    that block, is exactly 0, while out[:, 1] stays within 5% of the fp16
+    oracle.  Per-(row, 128-column) scales would keep the small block (out[:, 0]
+    within ~1% of the fp16 oracle, as fp8's do); a scale taken from the wrong
+    row would break out[:, 1]."""
     x, lg, wg, wu, wd, ref, q, k = scale_contrast_case(quantize_rows_int8)
     (qg, sg), (qu, su), (qd, sd) = q
     out = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k).float()
-    h_small = ref[:, 0].abs()
-    assert (h_small > 1e-3).all(), "the small block contributes"
+    assert (ref[:, 0].abs() > 1e-3).all(), "the small block contributes in fp16"
     big = ref[:, 1].abs().mean() / ref[:, 0].abs().mean()
     assert big > 300, f"block contrast only {float(big):.0f}x"
-    rel0 = float((out[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
+    assert float(out[:, 0].abs().max()) == 0.0
     rel1 = float((out[:, 1] - ref[:, 1]).norm() / ref[:, 1].norm())
-    assert rel0 < 5e-2 and rel1 < 5e-2, (rel0, rel1)
-    # the same data with one scale over both blocks loses the small block
-    out_row = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k, scale_block=256).float()
-    assert float(out_row[:, 0].abs().max()) == 0.0
+    assert rel1 < 5e-2, rel1
+    # the fp8 path keeps per-(row, 128-column) scales: the small block survives
+    from oracle import quantize_rows_fp8
+    x, lg, wg, wu, wd, ref, q8, k = scale_contrast_case(quantize_rows_fp8)
+    (qg, sg), (qu, su), (qd, sd) = q8
+    out8 = w8a8_forward(x, lg, qg, sg, qu, su, qd, sd, k, fmt="fp8").float()
+    rel0 = float((out8[:, 0] - ref[:, 0]).norm() / ref[:, 0].norm())
+    assert rel0 < 8e-2, rel0
+
+
+def test_w8a8_int8_invariant_under_intermediate_permutation():
+    """One scale over the whole row makes the int8 result independent of the
+    order of the I columns: permuting gate/up rows and w_down columns by the
+    same permutation (here one that moves columns across 128-column blocks)
+    gives a bit-identical output.  Per-block scales would not: the blocks'
+    maxima change."""
+    g = torch.Generator().manual_seed(12)
+    T, H, I, E, k = 24, 256, 384, 4, 2
+    x = torch.randn(T, H, generator=g).half()
+    lg = torch.randn(T, E, generator=g)
+    wg = (torch.randn(E, I, H, generator=g) * 0.05)
+    wu = (torch.randn(E, I, H, generator=g) * 0.05)
+    wg[:, :128] *= 8.0  # uneven column blocks, so per-block and per-row scales differ
+    wg, wu = wg.half(), wu.half()
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).half()
+    perm = torch.randperm(I, generator=g)
+    q = [quantize_rows_int8(w) for w in (wg, wu, wd)]
+    qp = [quantize_rows_int8(w) for w in (wg[:, perm], wu[:, perm], wd[:, :, perm])]
+    out = w8a8_forward(x, lg, *q[0], *q[1], *q[2], k)
+    outp = w8a8_forward(x, lg, *qp[0], *qp[1], *qp[2], k)
+    assert float(out.float().abs().max()) > 0 and torch.equal(out, outp)
+    # the same permutation moves fp8's per-(row, 128-column) block maxima, so
+    # its result changes: the check tells the two contracts apart
+    from oracle import quantize_rows_fp8
+    q8 = [quantize_rows_fp8(w) for w in (wg, wu, wd)]
+    q8p = [quantize_rows_fp8(w) for w in (wg[:, perm], wu[:, perm], wd[:, :, perm])]
+    o8 = w8a8_forward(x, lg, *q8[0], *q8[1], *q8[2], k, fmt="fp8")
+    o8p = w8a8_forward(x, lg, *q8p[0], *q8p[1], *q8p[2], k, fmt="fp8")
+    assert not torch.equal(o8, o8p)

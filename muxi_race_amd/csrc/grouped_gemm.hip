@@ -18,6 +18,12 @@
 
 #include <type_traits>
 
+// Stage 2 output through LDS as whole row segments (1) or direct 16-byte
+// pieces of 32 rows per store (0).
+#ifndef MOE_S2_STAGED_OUT
+#define MOE_S2_STAGED_OUT 1
+#endif
+
 namespace moe {
 
 template <int BM, int WAVES_M, int BN, int NW>
@@ -664,6 +670,19 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   };
   with_live<L::NBM>(live < 0 ? 0 : live, main_loop);
 
+  // Epilogue.  Each lane's accumulators hold 4-feature runs of one token row,
+  // so direct stores write 16 bytes of 32 rows per instruction.  Where the
+  // output tile fits the ring, it is first assembled in LDS and then stored
+  // as whole row segments, 16 bytes per lane (up to 512 bytes of one row per
+  // 32 lanes).  In LDS, 16-byte chunk c of tile row r sits at chunk slot
+  // c ^ (r & xm) (xm = chunks per row - 1, at most 15): the 16 rows one
+  // 8-byte write instruction covers per half-wave land on 16 different slots,
+  // and a row's chunks, read 16 at a time, on 16 different slots.
+  constexpr int kTileBytes = 2 * BM * BN;  // BM x BN, or 2 BM x BN / 2 when paired, fp16
+  constexpr bool kStaged = MOE_S2_STAGED_OUT != 0 && kTileBytes <= S * STAGE;
+  const int pitch = 2 * rw;               // bytes per row of the staged tile
+  const int xm = (rw / 8 - 1) & 15;
+  if constexpr (kStaged) __syncthreads();  // every wave is done with the ring
   _Float16* o = reinterpret_cast<_Float16*>(p.out);
 #pragma unroll
   for (int b = 0; b < L::NBM; ++b) {
@@ -674,7 +693,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
-        const int n = n0 + wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);
+        const int nl = wn * L::WTN + 32 * a + 8 * rg + 4 * (l >> 5);  // feature within the tile
+        const int n = n0 + nl;
         f32x4 sd = {1.0f, 1.0f, 1.0f, 1.0f};
         if constexpr (I8) sd = *reinterpret_cast<const f32x4*>(p.sd + (int64_t)e * p.H + n);
         f16x4 v;
@@ -686,8 +706,23 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           // select, never multiply, so NaN/Inf garbage in padding rows cannot leak
           v[q] = valid ? (_Float16)(y * wr[b]) : (_Float16)0.0f;
         }
-        *reinterpret_cast<f16x4*>(o + orow[b] * p.H + n) = v;
+        if constexpr (kStaged)
+          *reinterpret_cast<f16x4*>(smem + m * pitch + 16 * ((nl >> 3) ^ (m & xm)) + 2 * (nl & 7)) = v;
+        else *reinterpret_cast<f16x4*>(o + orow[b] * p.H + n) = v;
       }
+  }
+  if constexpr (kStaged) {
+    __syncthreads();
+    // fused: the item's valid rows (the first `actual`), each to its pair's
+    // output row; pre-routed: all rows, padding rows as the zeros above
+    const int shift = __builtin_ctz(rw / 8);  // 16-byte chunks per row: rw / 8, a power of two
+    const int rows_out = FUSED ? actual : rx;
+    for (int idx = threadIdx.x; idx < rows_out << shift; idx += 64 * NW) {
+      const int r = idx >> shift, c = idx & ((1 << shift) - 1);
+      const int64_t orr = FUSED ? (int64_t)p.sorted_ids[row0 + r] : (int64_t)(row0 + r);
+      *reinterpret_cast<u32x4*>(o + orr * p.H + n0 + 8 * c) =
+          *reinterpret_cast<const u32x4*>(smem + r * pitch + 16 * (c ^ (r & xm)));
+    }
   }
 }
 

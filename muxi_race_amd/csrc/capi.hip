@@ -37,7 +37,7 @@ int64_t cap_rows(int64_t T, int64_t k, int64_t E, int64_t bm) {
 }
 
 struct FusedLayout {
-  int64_t ids, w, sorted, bexp, gs, go, gpo, whist, h, hq, hs, xq, sx, ypair, total;
+  int64_t ids, w, sorted, bexp, gs, go, gpo, whist, h, hq, hs, xq, sx, ypair, pos, total;
 };
 
 // qt: moe::kQF16, kQI8 or kQF8.  The intermediate h is fp16 for fp16 and int8
@@ -62,7 +62,8 @@ FusedLayout fused_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, 
   L.hs = o; o += w8 ? up(rows * (i8 ? 1 : I / moe::kBN) * 4) : 0;  // int8 [rows]; fp8 [I/128][rows], block-major
   L.xq = o; o += w8 ? up(T * H) : 0;
   L.sx = o; o += w8 ? up(T * 4) : 0;
-  L.ypair = o; o += up(P * H * 2);
+  L.ypair = o; o += up(P * H * 2);                        // per-pair outputs, expert-sorted rows
+  L.pos = o; o += up(P * 4);                              // pair -> its y_pair row
   L.total = o;
   return L;
 }
@@ -385,6 +386,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.wd = (const char*)wd;
   p2.sd = sd;
   p2.out = ws + L.ypair;
+  p2.pos = (int32_t*)(ws + L.pos);
   p2.routed = wts;
   p2.routed_f16 = 0;
   p2.gs = gs;
@@ -400,7 +402,8 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.I = I;
   if ((rc = check_launch(moe::launch_stage2(p2, (int)bm2, qt, true, rows / bm2, s), "stage2"))) return rc;
   mark(5);
-  rc = check_launch(moe::launch_combine(ws + L.ypair, T, H, (int)ke, out, s, shard ? ids : nullptr, (int)e_begin, (int)E),
+  rc = check_launch(moe::launch_combine(ws + L.ypair, (const int32_t*)(ws + L.pos), T, H, (int)ke, out, s,
+                                        shard ? ids : nullptr, (int)e_begin, (int)E),
                     "combine");
   mark(6);
   return rc;

@@ -511,7 +511,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   const int e = w.e;
   if (e >= 0) {
     gpo_e = p.gpo[e];
-    go_e = FUSED ? 0 : p.go[e];
+    go_e = p.go[e];
     actual = p.gs[e] - (row0 - gpo_e);
     actual = actual < 0 ? 0 : (actual > rx ? rx : actual);
   }
@@ -566,8 +566,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) {
       const bool valid = xr0 + 32 * b + (l & 31) < actual;
-      orow[b] = valid ? pid[b] : 0;
+      // the pair's output row: its unpadded position in the expert-sorted
+      // order, so an item writes one contiguous run of rows; the combine
+      // finds it through pos[pair], written here once per row
+      orow[b] = (int64_t)go_e + (row0 - gpo_e) + xr0 + 32 * b + (l & 31);
       wr[b] = reinterpret_cast<const float*>(p.routed)[valid ? pid[b] : 0];
+      if (valid && n0 == 0 && wn == 0 && l < 32) p.pos[pid[b]] = (int32_t)orow[b];
       if constexpr (I8 && !F8) shv[b] = valid ? p.a_scale[row0 + xr0 + 32 * b + (l & 31)] : 0.0f;
     }
   } else {
@@ -713,13 +717,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   }
   if constexpr (kStaged) {
     __syncthreads();
-    // fused: the item's valid rows (the first `actual`), each to its pair's
-    // output row; pre-routed: all rows, padding rows as the zeros above
+    // fused: the item's valid rows (the first `actual`) to their unpadded
+    // expert-sorted rows; pre-routed: all rows, padding rows as the zeros above
     const int shift = __builtin_ctz(rw / 8);  // 16-byte chunks per row: rw / 8, a power of two
     const int rows_out = FUSED ? actual : rx;
     for (int idx = threadIdx.x; idx < rows_out << shift; idx += 64 * NW) {
       const int r = idx >> shift, c = idx & ((1 << shift) - 1);
-      const int64_t orr = FUSED ? (int64_t)p.sorted_ids[row0 + r] : (int64_t)(row0 + r);
+      const int64_t orr = FUSED ? (int64_t)go_e + (row0 - gpo_e) + r : (int64_t)(row0 + r);
       *reinterpret_cast<u32x4*>(o + orr * p.H + n0 + 8 * c) =
           *reinterpret_cast<const u32x4*>(smem + r * pitch + 16 * (c ^ (r & xm)));
     }

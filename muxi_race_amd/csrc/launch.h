@@ -47,7 +47,9 @@ struct Stage2Params {
   int64_t as_stride;        // fp8 only: rows of each a_scale block (>= padded rows)
   const char* wd;           // [E, H, I]
   const float* sd;          // 8-bit only: [E, H]
-  char* out;                // pre-routed: fp16 [P, H]; fused: fp16 [T*topk, H]
+  char* out;                // pre-routed: fp16 [P, H]; fused: fp16 [T*topk, H], row = the pair's
+                            // unpadded expert-sorted position go[e] + (row - gpo[e])
+  int32_t* pos;             // fused only: pos[pair] = that row (written by the first N tile's items)
   const void* routed;       // pre-routed: [V] raw order (fp32|fp16); fused: fp32 [T*topk]
   int routed_f16;
   const int32_t* gs;
@@ -106,7 +108,8 @@ hipError_t launch_router(const void* x, const void* w_router, const float* bias,
                          int k, int32_t* ids, float* w, float* logits, float* part, hipStream_t stream,
                          int e_shared = -1);
 // ids (may be null): sum only pairs whose expert is in [e_lo, e_lo + e_n).
-hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
+// y_pair row of pair t*k + j: pos[t*k + j].
+hipError_t launch_combine(const void* y_pair, const int32_t* pos, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream, const int32_t* ids = nullptr, int e_lo = 0, int e_n = 0);
 // Per-row 8-bit quantisation of an fp16 [R, K] matrix to the format qt
 // (kQI8 or kQF8): codes into q, amax / qmax into scale.  With `ids` set only

@@ -418,14 +418,16 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
 }
 
 // ---------------------------------------------------------------------------
-// Combine: out[t, :] = sum_j y_pair[t*k + j, :], fp32 in choice order -> fp16.
+// Combine: out[t, :] = sum_j y_pair[pos[t*k + j], :], fp32 in choice order ->
+// fp16 (Stage 2 writes each pair's row at its expert-sorted position pos).
 // One thread per 8 output columns.  The k rows are loaded in batches of 8
 // before they are summed (in choice order), so each thread keeps several loads
 // in flight; y_pair is read once, so the loads are non-temporal.  With `ids`
 // (an expert shard), only pairs routed to experts [e_lo, e_lo + e_n) are
 // summed: the others' rows were never written.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y, int64_t T,
+__global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y,
+                                                      const int32_t* __restrict__ pos, int64_t T,
                                                       int64_t H, int k, _Float16* __restrict__ out,
                                                       const int32_t* __restrict__ ids, int e_lo, int e_n) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -433,7 +435,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   if (idx >= T * cpr) return;
   const int64_t t = idx / cpr, c = idx % cpr;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const _Float16* src = y + (t * k) * H + 8 * c;
+  const _Float16* src = y + 8 * c;
+  const int32_t* prow = pos + t * k;
   constexpr int kBatch = 8;
   for (int j0 = 0; j0 < k; j0 += kBatch) {
     f16x8 v[kBatch];
@@ -443,7 +446,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
       in[u] = j0 + u < k && (!ids || (unsigned)ids[t * k + j0 + u] - (unsigned)e_lo < (unsigned)e_n);
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (in[u]) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)(j0 + u) * H));
+      if (in[u]) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)prow[j0 + u] * H));
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       if (in[u]) {
@@ -457,12 +460,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   *reinterpret_cast<f16x8*>(out + t * H + 8 * c) = r;
 }
 
-hipError_t launch_combine(const void* y_pair, int64_t T, int64_t H, int k, void* out,
+hipError_t launch_combine(const void* y_pair, const int32_t* pos, int64_t T, int64_t H, int k, void* out,
                           hipStream_t s, const int32_t* ids, int e_lo, int e_n) {
   const int64_t n = T * (H / 8);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                     reinterpret_cast<const _Float16*>(y_pair), T, H, k,
+                     reinterpret_cast<const _Float16*>(y_pair), pos, T, H, k,
                      reinterpret_cast<_Float16*>(out), ids, e_lo, e_n);
   return hipGetLastError();
 }

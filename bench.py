@@ -60,9 +60,28 @@ PEAK_I8_TOPS = 5000.0
 SEED = 20261201
 
 
-def make_inputs(name, dev, weights=None):
+def uniform_logits(T, E, k, rows):
+    """Router logits that give `rows` routed rows to each of the first
+    T*k/rows experts exactly: token t picks experts (k*t + j) mod (T*k/rows),
+    j < k, in that order (pairs k*t .. k*t + k - 1 enumerate every residue
+    T*k/rows apart)."""
+    import torch
+    if rows <= 0 or (T * k) % rows or not k <= T * k // rows <= E:
+        raise ValueError(f"--uniform-rows {rows}: T*k = {T * k} must split into between k and E experts")
+    Eu = T * k // rows
+    t = torch.arange(T)
+    logits = torch.zeros((T, E))
+    for j in range(k):
+        logits[t, (k * t + j) % Eu] = 10.0 - 0.01 * j
+    return logits
+
+
+def make_inputs(name, dev, weights=None, uniform_rows=0):
     """Seeded inputs of a config; ``weights`` (wg, wu, wd) of the right shape
-    are reused instead of generated (decode shares dsv3's dimensions)."""
+    are reused instead of generated (decode shares dsv3's dimensions).  With
+    ``uniform_rows`` the routing gives exactly that many rows to each of
+    T*k/uniform_rows experts (no bias): a diagnostic of the schedule's item
+    kinds, not a BASELINE workload."""
     import torch
     T, H, I, E, k, bias_kind = CONFIGS[name]
     g = torch.Generator(device="cpu").manual_seed(SEED)
@@ -73,6 +92,8 @@ def make_inputs(name, dev, weights=None):
         bias = (torch.randn((E,), generator=g) * 0.5).to(dev)
     elif bias_kind == "zipf":
         bias = (-1.2 * torch.log(torch.arange(E, dtype=torch.float32) + 1)).to(dev)
+    if uniform_rows:
+        logits, bias = uniform_logits(T, E, k, uniform_rows).to(dev), None
     if weights is not None:
         wg, wu, wd = weights
     else:
@@ -445,6 +466,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the extra legs: run_kernel on the reference's cases 1-3 ('prerouted') and the "
                          "other BASELINE configs ('configs')")
+    ap.add_argument("--uniform-rows", type=int, default=0,
+                    help="diagnostic: route exactly this many rows to each of T*k/rows experts "
+                         "(e.g. 128: one block per expert, 256: pairs); implies --no-extra")
     ap.add_argument("--only", choices=("prerouted", "configs"), default=None,
                     help="run only that extra leg (for profiling), printing its JSON")
     ap.add_argument("--probe-ring", action="store_true",
@@ -477,7 +501,7 @@ def main():
             res["calib_copy_gb_per_s"] = calib_copy(dev)
         print(json.dumps(res), flush=True)
         return
-    inp = make_inputs(args.config, dev)
+    inp = make_inputs(args.config, dev, uniform_rows=args.uniform_rows)
     T, H, I, E, k = (inp[n] for n in ("T", "H", "I", "E", "k"))
     w8 = (args.config == "w8a8" or args.w8a8 or args.fp8) and not args.fp16
     fmt = "fp8" if args.fp8 else "int8"
@@ -740,7 +764,7 @@ def main():
     copy_gbs = calib_copy(dev) if args.calib_copy else None
 
     extra_pr = extra_cf = None
-    if not args.no_extra and args.config == "dsv3" and not w8 and args.weights == "dense":
+    if not args.no_extra and args.config == "dsv3" and not w8 and args.weights == "dense" and not args.uniform_rows:
         extra_pr = bench_prerouted(L, dev, args.steps, max(args.warmup, 20), not args.no_check)
         extra_cf = run_configs(L, dev, args.steps, max(args.warmup, 20), (inp["wg"], inp["wu"], inp["wd"]))
 
@@ -764,7 +788,8 @@ def main():
                                + (f"W8A8 {fmt}" if w8 else "fp16"),
                    "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": k,
                    "block_m": bm or int(L.moe_pick_block_m(T, E, k)), "experts_touched": int(touched),
-                   "weight_layout": f"{fmt} dense" if w8 else args.weights},
+                   "weight_layout": f"{fmt} dense" if w8 else args.weights,
+                   **({"uniform_rows_per_expert": args.uniform_rows} if args.uniform_rows else {})},
         "gb_per_s": round(gbs, 1),
         "frac_mfma_peak": round(tflops / peak_c, 4),
         "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),

@@ -18,6 +18,11 @@
 
 #include <type_traits>
 
+// Stage 1 8-bit 256-row items on the split ring (1) or on two whole 64 KiB
+// stages (0).
+#ifndef MOE_S1_SPLIT
+#define MOE_S1_SPLIT 1
+#endif
 // Stage 2 output through LDS as whole row segments (1) or direct 16-byte
 // pieces of 32 rows per store (0).
 #ifndef MOE_S2_STAGED_OUT
@@ -64,6 +69,18 @@ __device__ __forceinline__ void with_live(int live, F&& f) {
 // One ring stage holds the tile's token rows, then its weight rows (Stage 1:
 // gate rows, then up rows), ROWS x 128 bytes in all, filled by one DmaTile;
 // fragment reads address it by stage row.
+//
+// Split ring (8-bit 256-row items, MOE_S1_SPLIT): instead of S whole stages the ring
+// is 5 slots of 32 KiB, each holding either the 256 token rows or the 256
+// weight rows of a K step, issued in the order T0 W0 W1 | T1 W2 | T2 W3 | ...
+// (after step j's barrier: T(j+1), then W(j+2)).  Weight rows (HBM misses)
+// are then issued two steps ahead and token rows (L2 hits) one, and while step
+// j's wait runs, W(j+1) is still queued behind T(j), so the memory pipeline
+// never drains at a step boundary (a two-stage ring of whole 64 KiB stages
+// drains there).  A/B at the w8a8 shape: Stage 1 int8 0.505 -> 0.496 ms, fp8
+// 0.474 -> 0.453 ms.  fp16 (mixtral) measured slower on it, 1.158 -> 1.197 ms:
+// its token rows, 4 MiB per expert, often come from beyond L2, and one step of
+// lead is not enough for them; it keeps the two-stage ring.
 template <int BM, int WAVES_M, int S, int NW, int QT, bool GATHER, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   constexpr bool I8 = QT != kQF16;  // 8-bit operands (int8 or fp8) with row scales
@@ -76,7 +93,10 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(!(PAIR && F8), "fp8 quantises h per 128-column tile: items must span 128 columns");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
-  __shared__ __attribute__((aligned(16))) char smem[S * STAGE];
+  constexpr bool SPLIT = MOE_S1_SPLIT != 0 && I8 && !PAIR && BM == 2 * kBN && NW == 8;
+  constexpr int HALF = (SPLIT ? BM : 0) * kRowBytes;  // one slot of the split ring: 32 KiB
+  using LDH = DmaTile<SPLIT ? BM : 8 * NW, NW>;       // split ring: 256 rows per slot
+  __shared__ __attribute__((aligned(16))) char smem[SPLIT ? 5 * HALF : S * STAGE];
 
   const int nt = (int)(p.I / kBN);
   Work w;
@@ -103,11 +123,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.w_es;
   const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.w_es;
 
-  LD ld;
-#pragma unroll
-  for (int i = 0; i < LD::NI; ++i) {
-    const int r = LD::row_of(i);
-    const char* src;
+  // tile row r of the stage: token rows [0, rx), gate rows, then up rows
+  auto row_src = [&](int r) -> const char* {
     if (r < rx) {
       int64_t src_row;
       if (GATHER) {
@@ -116,13 +133,22 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       } else {
         src_row = row0 + (r < actual ? r : 0);  // padding rows: the item's first row, a cache hit
       }
-      src = p.x + src_row * kbytes;
-    } else if (r < rx + rw) {
-      src = gexp + (int64_t)(n0 + r - rx) * p.w_ld;
-    } else {
-      src = uexp + (int64_t)(n0 + r - rx - rw) * p.w_ld;
+      return p.x + src_row * kbytes;
     }
-    ld.set(i, src);
+    if (r < rx + rw) return gexp + (int64_t)(n0 + r - rx) * p.w_ld;
+    return uexp + (int64_t)(n0 + r - rx - rw) * p.w_ld;
+  };
+  LD ld;
+  LDH ldt, ldw;  // split ring: token rows, weight rows
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int i = 0; i < LDH::NI; ++i) {
+      ldt.set(i, row_src(LDH::row_of(i)));
+      ldw.set(i, row_src(rx + LDH::row_of(i)));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < LD::NI; ++i) ld.set(i, row_src(LD::row_of(i)));
   }
 
   const int wave = threadIdx.x >> 6;
@@ -135,8 +161,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // overall than keeping siblings in step.)
   const int live = (actual - wm * L::WTM + 31) / 32;
   const int xr0 = wm * L::WTM;           // stage row of this wave's first token row
-  const int gr0 = rx + wn * L::WTN;      // ... of its first gate row
-  const int ur0 = rx + rw + wn * L::WTN; // ... of its first up row
+  // ... of its first gate / up row (split ring: rows of the weight slot)
+  const int gr0 = (SPLIT ? 0 : rx) + wn * L::WTN;
+  const int ur0 = (SPLIT ? 0 : rx) + rw + wn * L::WTN;
 
   // 8-bit: the dequantisation scales of this lane's token rows and output
   // features, loaded before the K loop so that their latency hides behind it
@@ -184,18 +211,40 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // hold routed rows (chosen once, outside the loop: a branch inside it would
   // move the accumulators out of AGPRs every step); padding-only blocks get no
   // LDS reads and no MFMAs.  Every variant issues the same loads and barriers.
+  // split ring: slot of the i-th issued half stage is i % 5; T(j) is issued
+  // i = j ? 2j + 1 : 0, W(j) i = j > 1 ? 2j : j + 1
+  auto slot = [&](int i) { return smem + (i % 5) * HALF; };
   auto main_loop = [&](auto nb_c) {
     constexpr int NB = decltype(nb_c)::value;
+    if constexpr (SPLIT) {
+      ldt.issue(slot(0), 0);
+      ldw.issue(slot(1), 0);
+      if (nk > 1) ldw.issue(slot(2), 1);
+    } else {
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s)
-      if (s < nk) ld.issue(smem + s * STAGE, s);
+      for (int s = 0; s < S - 1; ++s)
+        if (s < nk) ld.issue(smem + s * STAGE, s);
+    }
     int cur = 0;
     for (int ks = 0; ks < nk; ++ks) {
-      wait_stages<Q, S - 2>(nk - 1 - ks);
-      barrier_no_fence();
-      if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
-      const char* st = smem + cur * STAGE;
-      cur = cur + 1 == S ? 0 : cur + 1;
+      const char* st;   // token rows of step ks
+      const char* stw;  // weight rows of step ks
+      if constexpr (SPLIT) {
+        // T(ks) and W(ks) are done when at most W(ks + 1)'s loads are outstanding
+        if (ks + 1 < nk) wait_vmcnt<LDH::NI>();
+        else wait_vmcnt<0>();
+        barrier_no_fence();
+        if (ks + 1 < nk) ldt.issue(slot(2 * ks + 3), ks + 1);
+        if (ks + 2 < nk) ldw.issue(slot(2 * ks + 4), ks + 2);
+        st = slot(ks ? 2 * ks + 1 : 0);
+        stw = slot(ks > 1 ? 2 * ks : ks + 1);
+      } else {
+        wait_stages<Q, S - 2>(nk - 1 - ks);
+        barrier_no_fence();
+        if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
+        st = stw = smem + cur * STAGE;
+        cur = cur + 1 == S ? 0 : cur + 1;
+      }
       if constexpr (NB > 0) {
         // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
         // sub-step s+1 are in flight while the MFMAs of sub-step s run.
@@ -205,8 +254,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int b = 0; b < NB; ++b) xf[buf][b] = frag(st, xr0 + 32 * b, s);
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a) {
-            gf[buf][a] = frag(st, gr0 + 32 * a, s);
-            uf[buf][a] = frag(st, ur0 + 32 * a, s);
+            gf[buf][a] = frag(stw, gr0 + 32 * a, s);
+            uf[buf][a] = frag(stw, ur0 + 32 * a, s);
           }
         };
         if constexpr (F8) {

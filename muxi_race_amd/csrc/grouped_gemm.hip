@@ -18,6 +18,15 @@
 
 #include <type_traits>
 
+// Whole-stage rings of three or more stages issue the next stage's loads
+// spread over a step's sub-steps (1) or in one burst after the barrier (0).
+// A/B: mixtral Stage 2 0.680 -> 0.648 ms, dsv3 and the pre-routed cases level.
+// Two-stage rings (256-row items) keep the burst: spread there, a stage is
+// issued later in the step and arrives late (mixtral Stage 1 +10%, int8
+// Stage 2 +5%).
+#ifndef MOE_SPREAD_ISSUE
+#define MOE_SPREAD_ISSUE 1
+#endif
 // Stage 1 8-bit 256-row items on the split ring (1) or on two whole 64 KiB
 // stages (0).
 #ifndef MOE_S1_SPLIT
@@ -241,10 +250,18 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       } else {
         wait_stages<Q, S - 2>(nk - 1 - ks);
         barrier_no_fence();
-        if (ks + S - 1 < nk) ld.issue(smem + (cur == 0 ? S - 1 : cur - 1) * STAGE, ks + S - 1);
         st = stw = smem + cur * STAGE;
-        cur = cur + 1 == S ? 0 : cur + 1;
       }
+      // The next stage's loads (whole-stage ring): issued in one burst, or
+      // (rings of three or more stages, MOE_SPREAD_ISSUE) spread over the
+      // step's sub-steps so that no wave waits behind a long run of its own
+      // DMA issues before its MFMAs.
+      const bool pend = !SPLIT && ks + S - 1 < nk;
+      char* pbuf = smem + (cur == 0 ? S - 1 : cur - 1) * STAGE;
+      const int pk = ks + S - 1;
+      if constexpr (!SPLIT) cur = cur + 1 == S ? 0 : cur + 1;
+      constexpr bool kSpread = MOE_SPREAD_ISSUE != 0 && NB > 0 && S >= 3;
+      if (!kSpread && pend) ld.issue(pbuf, pk);
       if constexpr (NB > 0) {
         // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
         // sub-step s+1 are in flight while the MFMAs of sub-step s run.
@@ -264,6 +281,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int j = 0; j < 2; ++j) {
             load_frags(0, 2 * j);
             load_frags(1, 2 * j + 1);
+            if (kSpread && pend) ld.template issue_part<2>(pbuf, pk, j);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)
@@ -279,6 +297,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int s = 0; s < 4; ++s) {
             const int fb = s & 1;
             if (s < 3) load_frags(fb ^ 1, s + 1);
+            if (kSpread && pend) ld.template issue_part<4>(pbuf, pk, s);
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)
@@ -660,6 +679,14 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     else ld.issue(st, k);
     if constexpr (F8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
+  // part `part` of PARTS of issue(buf, k) (the scale row rides with part 0)
+  auto issue_part = [&](int buf, int k, auto parts_c, int part) {
+    constexpr int PARTS = decltype(parts_c)::value;
+    char* st = smem + buf * STAGE;
+    ld.template issue_part<PARTS>(st, k, part);
+    if constexpr (F8)
+      if (part == 0) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
+  };
   // K loop instantiated per count of live token blocks (see Stage 1).
   auto main_loop = [&](auto nb_c) {
     constexpr int NB = decltype(nb_c)::value;
@@ -670,7 +697,11 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     for (int ks = 0; ks < nk; ++ks) {
       wait_stages<Q, S - 2>(nk - 1 - ks);
       barrier_no_fence();
-      if (ks + S - 1 < nk) issue(cur == 0 ? S - 1 : cur - 1, ks + S - 1);
+      // the next stage's loads: one burst, or spread over the sub-steps (see Stage 1)
+      const bool pend = ks + S - 1 < nk;
+      const int pbuf = cur == 0 ? S - 1 : cur - 1, pk = ks + S - 1;
+      constexpr bool kSpread = MOE_SPREAD_ISSUE != 0 && NB > 0 && !STREAM && S >= 3;
+      if (!kSpread && pend) issue(pbuf, pk);
       const char* st = smem + cur * STAGE;
       cur = cur + 1 == S ? 0 : cur + 1;
       if constexpr (NB > 0) {
@@ -688,6 +719,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           for (int s = 0; s < 4; ++s) {
             const int fb = s & 1;
             if (s < 3) load_frags(fb ^ 1, s + 1);
+            if (kSpread && pend) issue_part(pbuf, pk, std::integral_constant<int, 4>{}, s);
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)
@@ -710,6 +742,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
           for (int j = 0; j < 2; ++j) {
             load_frags(0, 2 * j);
             load_frags(1, 2 * j + 1);
+            if (kSpread && pend) issue_part(pbuf, pk, std::integral_constant<int, 2>{}, j);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)

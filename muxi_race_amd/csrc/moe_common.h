@@ -149,6 +149,14 @@ struct DmaTile {
 #pragma unroll
     for (int i = 0; i < NI; ++i) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
   }
+  // The instructions i with i % PARTS == part of issue(lds, ks).
+  template <int PARTS>
+  __device__ __forceinline__ void issue_part(char* lds, int ks, int part) const {
+    const int w = wave_id();
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      if (i % PARTS == part) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+  }
   // As issue(), with tile rows from `weights_from` on loaded under the
   // streaming weight policy (kNoStream: none); an instruction's 8 rows never
   // straddle that boundary when it is a multiple of 8, so the choice is

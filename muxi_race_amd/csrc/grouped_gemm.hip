@@ -173,6 +173,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // ... of its first gate / up row (split ring: rows of the weight slot)
   const int gr0 = (SPLIT ? 0 : rx) + wn * L::WTN;
   const int ur0 = (SPLIT ? 0 : rx) + rw + wn * L::WTN;
+  const FragLane fl;
 
   // 8-bit: the dequantisation scales of this lane's token rows and output
   // features, loaded before the K loop so that their latency hides behind it
@@ -266,13 +267,14 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
         // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
         // sub-step s+1 are in flight while the MFMAs of sub-step s run.
         u32x4 xf[2][NB], gf[2][L::NBN], uf[2][L::NBN];
+        const uint32_t xb = row_base(st, xr0), gb = row_base(stw, gr0), ub = row_base(stw, ur0);
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) xf[buf][b] = frag(st, xr0 + 32 * b, s);
+          for (int b = 0; b < NB; ++b) xf[buf][b] = frag_at(xb + 4096 * b, fl.off[s]);
 #pragma unroll
           for (int a = 0; a < L::NBN; ++a) {
-            gf[buf][a] = frag(stw, gr0 + 32 * a, s);
-            uf[buf][a] = frag(stw, ur0 + 32 * a, s);
+            gf[buf][a] = frag_at(gb + 4096 * a, fl.off[s]);
+            uf[buf][a] = frag_at(ub + 4096 * a, fl.off[s]);
           }
         };
         if constexpr (F8) {
@@ -618,6 +620,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   const int live = (actual - wm * L::WTM + 31) / 32;  // see Stage 1
   const int xr0 = wm * L::WTM;       // stage row of this wave's first token row
   const int wr0 = rx + wn * L::WTN;  // ... of its first weight row
+  const FragLane fl;
 
   // Output row and routing weight of each of this lane's token rows, loaded
   // before the K loop so that their latency hides behind it.
@@ -706,11 +709,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       cur = cur + 1 == S ? 0 : cur + 1;
       if constexpr (NB > 0) {
         u32x4 af[2][NB], wf[2][L::NBN];
+        const uint32_t xb = row_base(st, xr0), wb = row_base(st, wr0);
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) af[buf][b] = frag(st, xr0 + 32 * b, s);
+          for (int b = 0; b < NB; ++b) af[buf][b] = frag_at(xb + 4096 * b, fl.off[s]);
 #pragma unroll
-          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag(st, wr0 + 32 * a, s);
+          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag_at(wb + 4096 * a, fl.off[s]);
         };
         if constexpr (!F8) {
           // fp16 (fp32 accumulation) or int8 (int32 accumulation)

@@ -179,6 +179,31 @@ __device__ __forceinline__ u32x4 frag(const char* lds, int row0, int s) {
   return *reinterpret_cast<const u32x4*>(lds + lds_swz(row0 + (l & 31), 2 * s + (l >> 5)));
 }
 
+// The same reads by 32-bit LDS address, for the K loops.  A fragment's first
+// tile row is a multiple of 32 there, so its row swizzle depends on the lane
+// alone (swz(r0 + (l & 31)) = swz(l & 31)) and its address splits into a
+// wave-uniform row base, lds + 128 * r0, and a per-lane offset for each K
+// sub-step.  With the base taken through readfirstlane (a scalar register,
+// recomputed per ring stage) and the four lane offsets held once, the
+// compiler keeps one VGPR per sub-step instead of hoisting one address per
+// fragment and sub-step out of the K loop.
+struct FragLane {
+  uint32_t off[4];
+  __device__ __forceinline__ FragLane() {
+    const int l = lane_id();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) off[s] = (uint32_t)lds_swz(l & 31, 2 * s + (l >> 5));
+  }
+};
+__device__ __forceinline__ uint32_t row_base(const char* lds, int row0) {
+  const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)lds;
+  return __builtin_amdgcn_readfirstlane(a + ((uint32_t)row0 << 7));
+}
+__device__ __forceinline__ u32x4 frag_at(uint32_t base, uint32_t lane_off) {
+  typedef __attribute__((address_space(3))) const u32x4 LdsVec;
+  return *(LdsVec*)(uintptr_t)(base + lane_off);
+}
+
 __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);

@@ -370,6 +370,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p1.E = (int)Ee;
   p1.H = H;
   p1.I = I;
+  p1.absorb = 1;  // taken by the instances and expert counts that support it
   if ((rc = check_launch(moe::launch_stage1(p1, (int)bm1, qt, true, rows / bm1, s), "stage1"))) return rc;
   // int8: h (fp16) -> per-row int8 codes + scales, for the routed rows only
   // (sorted id below the sentinel T * ke, row below gpo[E])
@@ -387,6 +388,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.sd = sd;
   p2.out = ws + L.ypair;
   p2.pos = (int32_t*)(ws + L.pos);
+  p2.absorb = 1;  // taken by the instances and expert counts that support it
   p2.routed = wts;
   p2.routed_f16 = 0;
   p2.gs = gs;

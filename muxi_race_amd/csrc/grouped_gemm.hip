@@ -29,6 +29,12 @@
 #endif
 // Stage 1 8-bit 256-row items on the split ring (1) or on two whole 64 KiB
 // stages (0).
+// Absorbed rows (see schedule_absorbed): fp16 256-row Stage 1 items and
+// 128-row paired Stage 2 items take an expert's last few rows instead of
+// giving them items of their own; 0 turns it off.
+#ifndef MOE_ABSORB
+#define MOE_ABSORB 1
+#endif
 #ifndef MOE_S1_SPLIT
 #define MOE_S1_SPLIT 1
 #endif
@@ -98,7 +104,13 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + 2 * kBN;
   using LD = DmaTile<ROWS, NW>;
-  constexpr int STAGE = ROWS * kRowBytes;
+  // Absorbed rows (fp16 256-row items, the two-stage ring): kAbsorbRows more
+  // token rows at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one
+  // 8-row instruction each (the ring waits for vmcnt(0), so the uneven count
+  // changes no wait).  Each wave multiplies them with one of its four weight
+  // blocks: 32 x 32 more outputs per wave, 1 MFMA per sub-step.
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && !PAIR && BM == 2 * kBN && NW == 8 && S == 2;
+  constexpr int STAGE = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(!(PAIR && F8), "fp8 quantises h per 128-column tile: items must span 128 columns");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
@@ -111,7 +123,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   Work w;
   // gathered (fused) launches follow the align metadata; direct (pre-routed)
   // ones map block -> expert through gidx
-  if (GATHER ? !schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w)
+  if (GATHER ? !schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w, p.gs,
+                         ABS && p.absorb != 0)
              : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, kBN, nt, PAIR, w)) return;
   const int e = w.e;
   if (e < 0) return;  // a block owned by no expert: Stage 2 writes its rows as 0
@@ -159,6 +172,18 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
 #pragma unroll
     for (int i = 0; i < LD::NI; ++i) ld.set(i, row_src(LD::row_of(i)));
   }
+  // absorbed rows: waves 0-3 each load 8 of them (rows past nar: the first one)
+  const int nar = ABS ? __builtin_amdgcn_readfirstlane(w.nar) : 0;
+  const bool adma = ABS && nar > 0 && wave_id() < 4;
+  const char* asrc = nullptr;
+  if (adma) {
+    const int r = 8 * wave_id() + (lane_id() >> 3);
+    const int pid = p.sorted_ids[w.ar0 + (r < nar ? r : 0)];
+    asrc = p.x + (int64_t)(pid / p.topk) * kbytes + ((((lane_id() & 7) ^ swz(ROWS + r)) & 7) << 4);
+  }
+  auto issue_abs = [&](char* stage, int k) {
+    if (adma) dma_to_lds<16>(asrc + (size_t)k * kRowBytes, stage + ROWS * kRowBytes + 1024 * wave_id());
+  };
 
   const int wave = threadIdx.x >> 6;
   const WavePos<L> wp(wave, rx != BM);
@@ -214,6 +239,10 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       ag[a][b] = Acc{};
       au[a][b] = Acc{};
     }
+  // absorbed rows x this wave's weight block: gate blocks 0, 1 of its half for
+  // wm = 0, 1, up blocks 0, 1 for wm = 2, 3
+  f32x16 aa = {};
+  const int awr0 = (wm < 2 ? gr0 : ur0) + 32 * (wm & 1);
 
   // S-stage ring: stages ks+1 .. ks+S-2 stay in flight while stage ks is used.
   constexpr int Q = LD::NI;  // loads per wave per stage
@@ -224,8 +253,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // split ring: slot of the i-th issued half stage is i % 5; T(j) is issued
   // i = j ? 2j + 1 : 0, W(j) i = j > 1 ? 2j : j + 1
   auto slot = [&](int i) { return smem + (i % 5) * HALF; };
-  auto main_loop = [&](auto nb_c) {
+  auto main_loop = [&](auto nb_c, auto abs_c) {
     constexpr int NB = decltype(nb_c)::value;
+    constexpr bool A = decltype(abs_c)::value;  // absorbed rows in this item
     if constexpr (SPLIT) {
       ldt.issue(slot(0), 0);
       ldw.issue(slot(1), 0);
@@ -233,7 +263,10 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     } else {
 #pragma unroll
       for (int s = 0; s < S - 1; ++s)
-        if (s < nk) ld.issue(smem + s * STAGE, s);
+        if (s < nk) {
+          ld.issue(smem + s * STAGE, s);
+          issue_abs(smem + s * STAGE, s);
+        }
     }
     int cur = 0;
     for (int ks = 0; ks < nk; ++ks) {
@@ -262,19 +295,29 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       const int pk = ks + S - 1;
       if constexpr (!SPLIT) cur = cur + 1 == S ? 0 : cur + 1;
       constexpr bool kSpread = MOE_SPREAD_ISSUE != 0 && NB > 0 && S >= 3;
-      if (!kSpread && pend) ld.issue(pbuf, pk);
-      if constexpr (NB > 0) {
+      if (!kSpread && pend) {
+        ld.issue(pbuf, pk);
+        issue_abs(pbuf, pk);
+      }
+      if constexpr (NB > 0 || A) {
         // Fragments double-buffered across the 4 K sub-steps: the LDS reads of
         // sub-step s+1 are in flight while the MFMAs of sub-step s run.
-        u32x4 xf[2][NB], gf[2][L::NBN], uf[2][L::NBN];
+        u32x4 xf[2][NB > 0 ? NB : 1], gf[2][L::NBN], uf[2][L::NBN], xa[2], wa[2];
         const uint32_t xb = row_base(st, xr0), gb = row_base(stw, gr0), ub = row_base(stw, ur0);
+        const uint32_t ab = A ? row_base(st, ROWS) : 0, wab = A ? row_base(stw, awr0) : 0;
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
           for (int b = 0; b < NB; ++b) xf[buf][b] = frag_at(xb + 4096 * b, fl.off[s]);
+          if constexpr (NB > 0) {
 #pragma unroll
-          for (int a = 0; a < L::NBN; ++a) {
-            gf[buf][a] = frag_at(gb + 4096 * a, fl.off[s]);
-            uf[buf][a] = frag_at(ub + 4096 * a, fl.off[s]);
+            for (int a = 0; a < L::NBN; ++a) {
+              gf[buf][a] = frag_at(gb + 4096 * a, fl.off[s]);
+              uf[buf][a] = frag_at(ub + 4096 * a, fl.off[s]);
+            }
+          }
+          if constexpr (A) {
+            xa[buf] = frag_at(ab, fl.off[s]);
+            wa[buf] = frag_at(wab, fl.off[s]);
           }
         };
         if constexpr (F8) {
@@ -308,12 +351,16 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
                 ag[a][b] = mma(gf[fb][a], xf[fb][b], ag[a][b]);
                 au[a][b] = mma(uf[fb][a], xf[fb][b], au[a][b]);
               }
+            if constexpr (A) aa = mma(wa[fb], xa[fb], aa);
           }
         }
       }
     }
   };
-  with_live<L::NBM>(live < 0 ? 0 : live, main_loop);
+  if (ABS && nar > 0)
+    with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::integral_constant<bool, ABS>{}); });
+  else
+    with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::false_type{}); });
   __syncthreads();  // every wave is done with the ring before LDS is reused
 
   const int l = lane_id();
@@ -355,6 +402,31 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
             }
             *reinterpret_cast<f16x4*>(hrow + n) = v;
           }
+      }
+    }
+    if constexpr (ABS) {
+      if (nar > 0) {
+        // absorbed rows: the up waves (wm = 2, 3) hand their block to the gate
+        // wave of the same features (wm - 2) through LDS; that one writes h
+        float* red = reinterpret_cast<float*>(smem);  // [wn][j][16][64]; the ring is free
+        if (wm >= 2) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) red[((wn * 2 + (wm & 1)) * 16 + q) * 64 + l] = aa[q];
+        }
+        __syncthreads();
+        const int m = l & 31;
+        if (wm < 2 && m < nar) {
+          _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(w.ar0 + m) * p.h_ld;
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const int n = n0 + wn * L::WTN + 32 * wm + 8 * rg + 4 * (l >> 5);
+            f16x4 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              v[q] = (_Float16)silu_mul(aa[4 * rg + q], red[((wn * 2 + wm) * 16 + 4 * rg + q) * 64 + l]);
+            *reinterpret_cast<f16x4*>(hrow + n) = v;
+          }
+        }
       }
     }
   } else {
@@ -561,7 +633,13 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + BN;
   using LD = DmaTile<ROWS, NW>;
-  constexpr int SCALES = ROWS * kRowBytes;                // fp8: row scales of the step
+  // Absorbed rows (fp16 fused 128-row paired items): kAbsorbRows more token
+  // rows at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
+  // instruction each (those waves wait for one more load per stage).  In a
+  // paired item the waves with wm < 2 (one per SIMD) multiply them with one of
+  // their two weight blocks; in a single item every wave does.
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && FUSED && PAIR && BM == 128 && NW == 8 && S == 3;
+  constexpr int SCALES = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;  // fp8: row scales of the step
   constexpr int STAGE = SCALES + (F8 ? 256 * NW : 0);
   static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
@@ -571,7 +649,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   Work w;
   // fused launches follow the align metadata; pre-routed ones map block ->
   // expert through gidx (every block of the launch is an item)
-  if (FUSED ? !schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, false, PAIR, w)
+  if (FUSED ? !schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, false, PAIR, w, p.gs,
+                        ABS && p.absorb != 0)
             : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, BN, nt, PAIR, w)) return;
   const int row0 = w.row0;
   const int n0 = w.n0;
@@ -613,10 +692,19 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     ld.set(i, r < rx ? p.a + (int64_t)(row0 + (r < actual ? r : 0)) * p.a_ld : dexp + (int64_t)(n0 + r - rx) * p.wd_ld);
   }
 
+  const int nar = ABS ? __builtin_amdgcn_readfirstlane(w.nar) : 0;  // absorbed rows
+  const bool adma = ABS && nar > 0 && wave_id() < 4;
+  const char* asrc = nullptr;
+  if (adma) {
+    const int r = 8 * wave_id() + (lane_id() >> 3);
+    asrc = p.a + (int64_t)(w.ar0 + (r < nar ? r : 0)) * p.a_ld + ((((lane_id() & 7) ^ swz(ROWS + r)) & 7) << 4);
+  }
+
   const int wave = threadIdx.x >> 6;
   const WavePos<L> wp(wave, rx != BM);
   const int wm = wp.wm, wn = wp.wn;
   const int l = lane_id();
+  const bool awave = nar > 0 && (rx == BM || wm < 2);  // this wave multiplies absorbed rows
   const int live = (actual - wm * L::WTM + 31) / 32;  // see Stage 1
   const int xr0 = wm * L::WTM;       // stage row of this wave's first token row
   const int wr0 = rx + wn * L::WTN;  // ... of its first weight row
@@ -666,6 +754,19 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) acc[a][b] = Acc{};
+  // absorbed rows x weight block (wm & 1) of this wave; their pair, output
+  // row and routing weight (lane l: absorbed row l % 32)
+  f32x16 aa = {};
+  const int awr0 = wr0 + 32 * (wm & 1);
+  int64_t aorow = 0;
+  float awr = 0.0f;
+  if (ABS && awave) {
+    const int m = l & 31;
+    const int pid = p.sorted_ids[w.ar0 + (m < nar ? m : 0)];
+    aorow = (int64_t)go_e + (w.ar0 - gpo_e) + m;
+    awr = m < nar ? reinterpret_cast<const float*>(p.routed)[pid] : 0.0f;
+    if (m < nar && n0 == 0 && wn == 0 && (wm & 1) == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
+  }
 
   // fp8: the row scales of K step ks (block-major layout, so contiguous) ride
   // in the same stage: wave w loads rows 64w..64w+63 (clamped inside the tile)
@@ -676,29 +777,38 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     scale_src = p.a_scale + row0 + (r < actual ? r : 0);
   }
   constexpr int Q = LD::NI + (F8 ? 1 : 0);
+  auto issue_abs = [&](char* st, int k) {
+    if (adma) dma_to_lds<16>(asrc + (size_t)k * kRowBytes, st + ROWS * kRowBytes + 1024 * wave_id());
+  };
   auto issue = [&](int buf, int k) {
     char* st = smem + buf * STAGE;
     if constexpr (STREAM) ld.issue(st, k, w.shared ? kNoStream : rx);
     else ld.issue(st, k);
+    issue_abs(st, k);
     if constexpr (F8) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
-  // part `part` of PARTS of issue(buf, k) (the scale row rides with part 0)
+  // part `part` of PARTS of issue(buf, k) (the scale row and the absorbed rows ride with part 0)
   auto issue_part = [&](int buf, int k, auto parts_c, int part) {
     constexpr int PARTS = decltype(parts_c)::value;
     char* st = smem + buf * STAGE;
     ld.template issue_part<PARTS>(st, k, part);
+    if (part == 0) issue_abs(st, k);
     if constexpr (F8)
       if (part == 0) dma_to_lds<4>(scale_src + (int64_t)k * p.as_stride, st + SCALES + 256 * wave_id());
   };
-  // K loop instantiated per count of live token blocks (see Stage 1).
-  auto main_loop = [&](auto nb_c) {
+  const int q_wave = Q + (adma ? 1 : 0);  // loads per stage of this wave
+  // K loop instantiated per count of live token blocks (see Stage 1) and
+  // whether this wave multiplies absorbed rows.
+  auto main_loop = [&](auto nb_c, auto abs_c) {
     constexpr int NB = decltype(nb_c)::value;
+    constexpr bool A = decltype(abs_c)::value;
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
       if (s < nk) issue(s, s);
     int cur = 0;
     for (int ks = 0; ks < nk; ++ks) {
-      wait_stages<Q, S - 2>(nk - 1 - ks);
+      if constexpr (ABS) wait_stages_q<Q + 1, S - 2>(q_wave, nk - 1 - ks);
+      else wait_stages<Q, S - 2>(nk - 1 - ks);
       barrier_no_fence();
       // the next stage's loads: one burst, or spread over the sub-steps (see Stage 1)
       const bool pend = ks + S - 1 < nk;
@@ -707,14 +817,21 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       if (!kSpread && pend) issue(pbuf, pk);
       const char* st = smem + cur * STAGE;
       cur = cur + 1 == S ? 0 : cur + 1;
-      if constexpr (NB > 0) {
-        u32x4 af[2][NB], wf[2][L::NBN];
+      if constexpr (NB > 0 || A) {
+        u32x4 af[2][NB > 0 ? NB : 1], wf[2][L::NBN], xa[2], wa[2];
         const uint32_t xb = row_base(st, xr0), wb = row_base(st, wr0);
+        const uint32_t ab = A ? row_base(st, ROWS) : 0, wab = A ? row_base(st, awr0) : 0;
         auto load_frags = [&](int buf, int s) {
 #pragma unroll
           for (int b = 0; b < NB; ++b) af[buf][b] = frag_at(xb + 4096 * b, fl.off[s]);
+          if constexpr (NB > 0) {
 #pragma unroll
-          for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag_at(wb + 4096 * a, fl.off[s]);
+            for (int a = 0; a < L::NBN; ++a) wf[buf][a] = frag_at(wb + 4096 * a, fl.off[s]);
+          }
+          if constexpr (A) {
+            xa[buf] = frag_at(ab, fl.off[s]);
+            wa[buf] = frag_at(wab, fl.off[s]);
+          }
         };
         if constexpr (!F8) {
           // fp16 (fp32 accumulation) or int8 (int32 accumulation)
@@ -729,6 +846,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
             for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
               for (int b = 0; b < NB; ++b) acc[a][b] = mma(wf[fb][a], af[fb][b], acc[a][b]);
+            if constexpr (A) aa = mma(wa[fb], xa[fb], aa);
           }
         } else {
           // One K step of fp8 operands is one 128-column scale block of the
@@ -758,7 +876,10 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       }
     }
   };
-  with_live<L::NBM>(live < 0 ? 0 : live, main_loop);
+  if (ABS && awave)
+    with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::integral_constant<bool, ABS>{}); });
+  else
+    with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::false_type{}); });
 
   // Epilogue.  Each lane's accumulators hold 4-feature runs of one token row,
   // so direct stores write 16 bytes of 32 rows per instruction.  Where the
@@ -812,6 +933,19 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       const int64_t orr = FUSED ? (int64_t)go_e + (row0 - gpo_e) + r : (int64_t)(row0 + r);
       *reinterpret_cast<u32x4*>(o + orr * p.H + n0 + 8 * c) =
           *reinterpret_cast<const u32x4*>(smem + r * pitch + 16 * (c ^ (r & xm)));
+    }
+  }
+  if constexpr (ABS) {
+    // absorbed rows: their unpadded expert-sorted output rows, stored directly
+    if (awave && (l & 31) < nar) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int n = n0 + wn * L::WTN + 32 * (wm & 1) + 8 * rg + 4 * (l >> 5);
+        f16x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (_Float16)(aa[4 * rg + q] * awr);
+        *reinterpret_cast<f16x4*>(o + aorow * p.H + n) = v;
+      }
     }
   }
 }

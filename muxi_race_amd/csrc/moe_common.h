@@ -74,6 +74,31 @@ __device__ __forceinline__ void wait_stages(int ahead) {
   }
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n known only at run time: the
+// immediate is picked by scalar branches; n above MAX waits for MAX instead
+// (a stricter wait).
+template <int MAX>
+__device__ __forceinline__ void wait_vmcnt_rt(int n) {
+  if constexpr (MAX <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= MAX) wait_vmcnt<MAX>();
+    else wait_vmcnt_rt<MAX - 1>(n);
+  }
+}
+
+// wait_stages for waves that issue q <= Q loads per stage (q wave-uniform,
+// the same for every stage of the wave).
+template <int Q, int N>
+__device__ __forceinline__ void wait_stages_q(int q, int ahead) {
+  if constexpr (N <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= N) wait_vmcnt_rt<Q * N>(q * N);
+    else wait_stages_q<Q, N - 1>(q, ahead);
+  }
+}
+
 // Workgroup barrier without a memory fence.  __syncthreads() would first wait
 // for every outstanding vector-memory operation (vmcnt(0)), which includes the
 // direct-to-LDS loads of the stages still in flight; the pipelines below wait
@@ -333,10 +358,32 @@ struct Work {
   int n0;       // first output feature of the tile
   int bn;       // BN, or BN/2 for a paired item
   bool shared;  // other items of this launch read the same weight rows
+  int ar0 = 0;  // absorbed rows (see below): first sorted row ...
+  int nar = 0;  // ... and count (0: none)
 };
 
+// Absorbed rows.  An expert's rows rarely fill its last block: at mixtral's
+// ~512 rows per expert, 256-row blocks leave 5 of 8 experts a third block of
+// 2-30 rows, and its items (a quarter of Stage 1's) each stream a whole weight
+// tile for those few rows.  With absorption on, an expert whose last block
+// holding routed rows holds at most kAbsorbRows of them, after at least one
+// other block, gets no items for that block (nor for an empty block after it,
+// which the 256-row padding leaves to 128-row launches): its first item group
+// -- block 0's item, or both halves of pair 0 when paired -- takes those rows
+// as w.nar extra token rows from sorted row w.ar0, against the weight tile it
+// streams anyway.  The item count drops by those blocks' items, and the
+// launch's items are renumbered so that the 8 XCD chunks stay even.  The
+// expert scan runs in one wave pass, so absorption needs E <= 64.
+constexpr int kAbsorbRows = 32;
+
+__device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
+                                                  const int32_t* __restrict__ gs, int E, int BM, int BN,
+                                                  int nt, int host_blocks, bool pair, Work& w);
+
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
-                                         int nt, int host_blocks, bool tail, bool pair, Work& w) {
+                                         int nt, int host_blocks, bool tail, bool pair, Work& w,
+                                         const int32_t* __restrict__ gs = nullptr, bool absorb = false) {
+  if (absorb && !tail && E <= 64) return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, w);
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
   const int total_blocks = tail ? host_blocks : expert_blocks;
@@ -388,6 +435,63 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
     w.n0 = t * BN;
   }
   return (w.row0 + w.rows) / BM <= host_blocks && t < nt;
+}
+
+// schedule() with absorbed rows (E <= 64, no ownerless tail items).  Lane l
+// scans expert l: nb blocks, of which d (the last block with routed rows, if
+// absorbed, and any empty block after it) get no items.  Expert l's items
+// start at (gpo[l]/BM - sum of d below l) * nt, counted with two ballots.
+__device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
+                                                  const int32_t* __restrict__ gs, int E, int BM, int BN,
+                                                  int nt, int host_blocks, bool pair, Work& w) {
+  const int l = lane_id();
+  int b0 = 0, nb = 0, d = 0;
+  if (l < E) {
+    b0 = gpo[l] / BM;
+    nb = gpo[l + 1] / BM - b0;
+    const int n = gs[l];
+    const int v = (n + BM - 1) / BM;  // blocks holding routed rows
+    if (v >= 2 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3) d = nb - (v - 1);
+  }
+  const uint64_t m1 = __ballot(d & 1), m2 = __ballot((d >> 1) & 1);
+  int expert_blocks = gpo[E] / BM;
+  expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
+  const int total = (expert_blocks - __popcll(m1) - 2 * __popcll(m2)) * nt;
+  const int per = (total + kNumXcd - 1) / kNumXcd;
+  const int slot = g / kNumXcd;
+  const int v = (g % kNumXcd) * per + slot;
+  if (total <= 0 || slot >= per || v >= total) return false;
+  const uint64_t below = (1ull << l) - 1;  // l <= 63
+  const int start = (b0 - __popcll(m1 & below) - 2 * __popcll(m2 & below)) * nt;
+  const int e = __popcll(__ballot(l < E && start <= v)) - 1;
+  if (e < 0) return false;  // only with inconsistent metadata (gpo[0] > 0)
+  const int eb0 = __shfl(b0, e), enb = __shfl(nb, e), ed = __shfl(d, e), estart = __shfl(start, e);
+  const int nm = enb - ed;  // blocks with items
+  if (nm <= 0) return false;
+  const int local = v - estart;
+  const int t = local / nm;  // N tile
+  const int r = local % nm;  // item within tile t
+  const int P = pair ? nm / 2 : 0;
+  w.e = e;
+  w.shared = pair ? nm > 2 : nm > 1;
+  if (r < 2 * P) {
+    w.rows = 2 * BM;
+    w.row0 = (eb0 + 2 * (r % P)) * BM;
+    w.bn = BN / 2;
+    w.n0 = (2 * t + r / P) * (BN / 2);
+  } else {
+    w.rows = BM;
+    w.row0 = (eb0 + r) * BM;
+    w.bn = BN;
+    w.n0 = t * BN;
+  }
+  w.ar0 = 0;
+  w.nar = 0;
+  if (ed > 0 && (P > 0 ? (r < 2 * P && r % P == 0) : r == 0)) {
+    w.ar0 = (eb0 + nm) * BM;
+    w.nar = gs[e] - nm * BM;  // 1 .. kAbsorbRows
+  }
+  return (w.row0 + w.rows) / BM <= host_blocks && (w.nar == 0 || w.ar0 / BM < host_blocks) && t < nt;
 }
 
 // Pre-routed launches (the reference operator): block b's expert is

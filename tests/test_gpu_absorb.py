@@ -1,0 +1,72 @@
+"""GPU parity of absorbed rows.  When an expert's last block holds at most 32
+routed rows (after at least one other block), the schedule gives that block
+no items: the expert's first item group takes those rows as extra token rows
+(moe_common.h schedule_absorbed; fp16 Stage 1 256-row items and Stage 2
+128-row paired items, E <= 64).  Exact per-expert counts straddle the rule:
+1 and 32 rows past a block boundary are absorbed, 33 are not, and so are
+single-block experts, empty ones and exact multiples.  They run under the
+256-row padding (block_m 0 picks it here: H % 256 == 0, >= 192 rows per
+expert) and the 128-row padding, with top-1 and top-2 routing.  Every output
+is compared whole with the oracle, from a NaN-poisoned buffer."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close
+from oracle import fused_moe_forward, route_topk
+
+pytestmark = pytest.mark.gpu
+
+# per-expert routed rows; with 256-row blocks 257, 288, 513, 543 are absorbed
+# in Stage 1, and with 128-row blocks 257, 288, 513, 543, 160, 385 in Stage 2
+COUNTS = [257, 288, 289, 545, 513, 543, 256, 1, 0, 33, 160, 161, 385, 417]
+H, I = 256, 256
+
+
+def _inputs(k, seed):
+    """x, logits and weights whose top-k routing gives expert e exactly
+    COUNTS[e] pairs (k = 2: the two experts of a token differ)."""
+    g = torch.Generator().manual_seed(seed)
+    E = len(COUNTS)
+    slots = np.repeat(np.arange(E), COUNTS)  # expert-sorted pair slots
+    P = len(slots)
+    assert P % k == 0 and max(COUNTS) < P // k
+    T = P // k
+    logits = torch.randn(T, E, generator=g) * 0.1
+    perm = torch.randperm(T, generator=g).numpy()  # tokens in random order
+    for j in range(k):
+        # token perm[i] takes slot i + j*T: an expert's run is shorter than T,
+        # so the k slots of a token name k different experts
+        logits[perm, torch.from_numpy(slots[j * T:(j + 1) * T])] += 8.0 - j
+    x = torch.randn(T, H, generator=g).half()
+    wg = (torch.randn(E, I, H, generator=g) * 0.05).half()
+    wu = (torch.randn(E, I, H, generator=g) * 0.05).half()
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).half()
+    ids, _ = route_topk(logits.numpy(), k, None)
+    np.testing.assert_array_equal(np.bincount(ids.ravel(), minlength=E), COUNTS)
+    return x, logits, wg, wu, wd
+
+
+@pytest.mark.parametrize("k", [1, 2])
+@pytest.mark.parametrize("bm", [0, 128])
+def test_absorbed_rows_full_output(k, bm):
+    from muxi_race_amd import fused_moe
+    x, logits, wg, wu, wd = _inputs(k, seed=31 + k)
+    T = x.shape[0]
+    out = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    out = fused_moe(x.cuda(), logits.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), k, block_m=bm, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
+    ref = fused_moe_forward(x, logits, wg, wu, wd, k)
+    assert_close(out, ref, what=f"absorbed rows k={k} bm={bm}")
+
+
+def test_absorbed_rows_repeatable():
+    """Two calls give bitwise the same output (the absorbed rows' items and
+    the rest are fixed by the metadata alone)."""
+    from muxi_race_amd import fused_moe
+    x, logits, wg, wu, wd = (t.cuda() for t in _inputs(2, seed=40))
+    a = fused_moe(x, logits, wg, wu, wd, 2)
+    b = fused_moe(x, logits, wg, wu, wd, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -104,12 +104,13 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + 2 * kBN;
   using LD = DmaTile<ROWS, NW>;
-  // Absorbed rows (fp16 256-row items, the two-stage ring): kAbsorbRows more
-  // token rows at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one
-  // 8-row instruction each (the ring waits for vmcnt(0), so the uneven count
-  // changes no wait).  Each wave multiplies them with one of its four weight
-  // blocks: 32 x 32 more outputs per wave, 1 MFMA per sub-step.
-  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && !PAIR && BM == 2 * kBN && NW == 8 && S == 2;
+  // Absorbed rows (fp16, gathered; 256-row items on the two-stage ring and
+  // 128-row paired items on the three-stage one): kAbsorbRows more token rows
+  // at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
+  // instruction each (those waves wait for one more load per stage).  A wave
+  // multiplies them with one of its weight blocks: 1 MFMA per sub-step.
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && GATHER && NW == 8 &&
+                       ((!PAIR && BM == 2 * kBN && S == 2) || (PAIR && BM == kBN && S == 3));
   constexpr int STAGE = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(!(PAIR && F8), "fp8 quantises h per 128-column tile: items must span 128 columns");
@@ -239,10 +240,17 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       ag[a][b] = Acc{};
       au[a][b] = Acc{};
     }
-  // absorbed rows x this wave's weight block: gate blocks 0, 1 of its half for
-  // wm = 0, 1, up blocks 0, 1 for wm = 2, 3
+  // absorbed rows x one weight block of this wave.  256-row items (two gate
+  // and two up blocks per wave): every wave, gate blocks 0, 1 for wm = 0, 1,
+  // up blocks 0, 1 for wm = 2, 3.  128-row items (one of each): the gate
+  // block for even wm, the up block for odd wm, on every wave of a single
+  // item and on wm < 2 (one wave per SIMD) of a paired one.
   f32x16 aa = {};
-  const int awr0 = (wm < 2 ? gr0 : ur0) + 32 * (wm & 1);
+  const bool awave = ABS && nar > 0 && (L::NBN == 2 || rx == BM || wm < 2);
+  const bool agate = L::NBN == 2 ? wm < 2 : (wm & 1) == 0;
+  const int aj = L::NBN == 2 ? (wm & 1) : 0;   // block among the wave's gate / up blocks
+  const int awr0 = (agate ? gr0 : ur0) + 32 * aj;
+  const int q_wave = LD::NI + (adma ? 1 : 0);  // loads per stage of this wave
 
   // S-stage ring: stages ks+1 .. ks+S-2 stay in flight while stage ks is used.
   constexpr int Q = LD::NI;  // loads per wave per stage
@@ -282,7 +290,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
         st = slot(ks ? 2 * ks + 1 : 0);
         stw = slot(ks > 1 ? 2 * ks : ks + 1);
       } else {
-        wait_stages<Q, S - 2>(nk - 1 - ks);
+        if constexpr (ABS) wait_stages_q<Q + 1, S - 2>(q_wave, nk - 1 - ks);
+        else wait_stages<Q, S - 2>(nk - 1 - ks);
         barrier_no_fence();
         st = stw = smem + cur * STAGE;
       }
@@ -342,7 +351,10 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
           for (int s = 0; s < 4; ++s) {
             const int fb = s & 1;
             if (s < 3) load_frags(fb ^ 1, s + 1);
-            if (kSpread && pend) ld.template issue_part<4>(pbuf, pk, s);
+            if (kSpread && pend) {
+              ld.template issue_part<4>(pbuf, pk, s);
+              if (s == 0) issue_abs(pbuf, pk);
+            }
             __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
             for (int a = 0; a < L::NBN; ++a)
@@ -357,7 +369,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
       }
     }
   };
-  if (ABS && nar > 0)
+  if (awave)
     with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::integral_constant<bool, ABS>{}); });
   else
     with_live<L::NBM>(live < 0 ? 0 : live, [&](auto nb_c) { main_loop(nb_c, std::false_type{}); });
@@ -406,24 +418,25 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
     }
     if constexpr (ABS) {
       if (nar > 0) {
-        // absorbed rows: the up waves (wm = 2, 3) hand their block to the gate
-        // wave of the same features (wm - 2) through LDS; that one writes h
-        float* red = reinterpret_cast<float*>(smem);  // [wn][j][16][64]; the ring is free
-        if (wm >= 2) {
+        // absorbed rows: each up wave hands its block through LDS to the gate
+        // wave of the same features (same wn and block), which writes h
+        float* red = reinterpret_cast<float*>(smem);  // [wn * NBN + j][16][64]; the ring is free
+        const int aslot = wn * L::NBN + aj;
+        if (awave && !agate) {
 #pragma unroll
-          for (int q = 0; q < 16; ++q) red[((wn * 2 + (wm & 1)) * 16 + q) * 64 + l] = aa[q];
+          for (int q = 0; q < 16; ++q) red[(aslot * 16 + q) * 64 + l] = aa[q];
         }
         __syncthreads();
         const int m = l & 31;
-        if (wm < 2 && m < nar) {
+        if (awave && agate && m < nar) {
           _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(w.ar0 + m) * p.h_ld;
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
-            const int n = n0 + wn * L::WTN + 32 * wm + 8 * rg + 4 * (l >> 5);
+            const int n = n0 + wn * L::WTN + 32 * aj + 8 * rg + 4 * (l >> 5);
             f16x4 v;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              v[q] = (_Float16)silu_mul(aa[4 * rg + q], red[((wn * 2 + wm) * 16 + 4 * rg + q) * 64 + l]);
+              v[q] = (_Float16)silu_mul(aa[4 * rg + q], red[(aslot * 16 + 4 * rg + q) * 64 + l]);
             *reinterpret_cast<f16x4*>(hrow + n) = v;
           }
         }

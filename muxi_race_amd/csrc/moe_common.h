@@ -373,8 +373,10 @@ struct Work {
 // as w.nar extra token rows from sorted row w.ar0, against the weight tile it
 // streams anyway.  The item count drops by those blocks' items, and the
 // launch's items are renumbered so that the 8 XCD chunks stay even.  The
-// expert scan runs in one wave pass, so absorption needs E <= 64.
+// expert scan keeps 4 values per chunk of 64 experts in registers, so
+// absorption needs E <= kAbsorbMaxE.
 constexpr int kAbsorbRows = 32;
+constexpr int kAbsorbMaxE = 256;
 
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
@@ -383,7 +385,7 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
                                          int nt, int host_blocks, bool tail, bool pair, Work& w,
                                          const int32_t* __restrict__ gs = nullptr, bool absorb = false) {
-  if (absorb && !tail && E <= 64) return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, w);
+  if (absorb && !tail && E <= kAbsorbMaxE) return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, w);
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
   const int total_blocks = tail ? host_blocks : expert_blocks;
@@ -437,35 +439,61 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
   return (w.row0 + w.rows) / BM <= host_blocks && t < nt;
 }
 
-// schedule() with absorbed rows (E <= 64, no ownerless tail items).  Lane l
-// scans expert l: nb blocks, of which d (the last block with routed rows, if
-// absorbed, and any empty block after it) get no items.  Expert l's items
-// start at (gpo[l]/BM - sum of d below l) * nt, counted with two ballots.
+// schedule() with absorbed rows (E <= kAbsorbMaxE, no ownerless tail items).
+// Lane l scans expert 64c + l of chunk c: nb blocks, of which d (the last
+// block with routed rows, if absorbed, and any empty block after it) get no
+// items.  Expert e's items start at (gpo[e]/BM - sum of d below e) * nt,
+// counted with two ballots per chunk; the selected expert is the last whose
+// first item is <= the workgroup's item.
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
                                                   int nt, int host_blocks, bool pair, Work& w) {
+  constexpr int C = kAbsorbMaxE / 64;
   const int l = lane_id();
-  int b0 = 0, nb = 0, d = 0;
-  if (l < E) {
-    b0 = gpo[l] / BM;
-    nb = gpo[l + 1] / BM - b0;
-    const int n = gs[l];
-    const int v = (n + BM - 1) / BM;  // blocks holding routed rows
-    if (v >= 2 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3) d = nb - (v - 1);
+  int cb0[C], cnb[C], cd[C];
+  uint64_t cm1[C], cm2[C];
+  int dtot = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int e = 64 * c + l;
+    int b0 = 0, nb = 0, d = 0;
+    if (e < E) {
+      b0 = gpo[e] / BM;
+      nb = gpo[e + 1] / BM - b0;
+      const int n = gs[e];
+      const int v = (n + BM - 1) / BM;  // blocks holding routed rows
+      if (v >= 2 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3) d = nb - (v - 1);
+    }
+    cb0[c] = b0;
+    cnb[c] = nb;
+    cd[c] = d;
+    cm1[c] = __ballot(d & 1);
+    cm2[c] = __ballot((d >> 1) & 1);
+    dtot += __popcll(cm1[c]) + 2 * __popcll(cm2[c]);
   }
-  const uint64_t m1 = __ballot(d & 1), m2 = __ballot((d >> 1) & 1);
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
-  const int total = (expert_blocks - __popcll(m1) - 2 * __popcll(m2)) * nt;
+  const int total = (expert_blocks - dtot) * nt;
   const int per = (total + kNumXcd - 1) / kNumXcd;
   const int slot = g / kNumXcd;
   const int v = (g % kNumXcd) * per + slot;
   if (total <= 0 || slot >= per || v >= total) return false;
   const uint64_t below = (1ull << l) - 1;  // l <= 63
-  const int start = (b0 - __popcll(m1 & below) - 2 * __popcll(m2 & below)) * nt;
-  const int e = __popcll(__ballot(l < E && start <= v)) - 1;
+  int e = -1, eb0 = 0, enb = 0, ed = 0, estart = 0, carry = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int start = (cb0[c] - carry - __popcll(cm1[c] & below) - 2 * __popcll(cm2[c] & below)) * nt;
+    const int k = __popcll(__ballot(64 * c + l < E && start <= v));
+    if (k > 0) {  // wave-uniform
+      e = 64 * c + k - 1;
+      eb0 = __shfl(cb0[c], k - 1);
+      enb = __shfl(cnb[c], k - 1);
+      ed = __shfl(cd[c], k - 1);
+      estart = __shfl(start, k - 1);
+    }
+    carry += __popcll(cm1[c]) + 2 * __popcll(cm2[c]);
+  }
   if (e < 0) return false;  // only with inconsistent metadata (gpo[0] > 0)
-  const int eb0 = __shfl(b0, e), enb = __shfl(nb, e), ed = __shfl(d, e), estart = __shfl(start, e);
   const int nm = enb - ed;  // blocks with items
   if (nm <= 0) return false;
   const int local = v - estart;

@@ -23,14 +23,14 @@ COUNTS = [257, 288, 289, 545, 513, 543, 256, 1, 0, 33, 160, 161, 385, 417]
 H, I = 256, 256
 
 
-def _inputs(k, seed):
+def _inputs(k, seed, counts=COUNTS):
     """x, logits and weights whose top-k routing gives expert e exactly
-    COUNTS[e] pairs (k = 2: the two experts of a token differ)."""
+    counts[e] pairs (k = 2: the two experts of a token differ)."""
     g = torch.Generator().manual_seed(seed)
-    E = len(COUNTS)
-    slots = np.repeat(np.arange(E), COUNTS)  # expert-sorted pair slots
+    E = len(counts)
+    slots = np.repeat(np.arange(E), counts)  # expert-sorted pair slots
     P = len(slots)
-    assert P % k == 0 and max(COUNTS) < P // k
+    assert P % k == 0 and max(counts) < P // k
     T = P // k
     logits = torch.randn(T, E, generator=g) * 0.1
     perm = torch.randperm(T, generator=g).numpy()  # tokens in random order
@@ -43,7 +43,7 @@ def _inputs(k, seed):
     wu = (torch.randn(E, I, H, generator=g) * 0.05).half()
     wd = (torch.randn(E, H, I, generator=g) * 0.05).half()
     ids, _ = route_topk(logits.numpy(), k, None)
-    np.testing.assert_array_equal(np.bincount(ids.ravel(), minlength=E), COUNTS)
+    np.testing.assert_array_equal(np.bincount(ids.ravel(), minlength=E), counts)
     return x, logits, wg, wu, wd
 
 
@@ -59,6 +59,25 @@ def test_absorbed_rows_full_output(k, bm):
     assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
     ref = fused_moe_forward(x, logits, wg, wu, wd, k)
     assert_close(out, ref, what=f"absorbed rows k={k} bm={bm}")
+
+
+def test_absorbed_rows_many_experts():
+    """E = 150 (the expert scan's third chunk), top-2, the default block_m
+    (128-row padding at ~130 rows per expert): Stage 1 paired 128-row items
+    absorb too.  Experts of 129-160 rows (one block and up to 32 rows) and of
+    257-288 (two blocks and up to 32) next to ones that stay as they are."""
+    from muxi_race_amd import fused_moe
+    rng = np.random.default_rng(5)
+    counts = list(COUNTS) + [int(rng.choice([0, rng.integers(1, 40), rng.integers(129, 161), rng.integers(161, 257),
+                                             rng.integers(257, 289)])) for _ in range(136)]
+    counts[-1] += sum(counts) % 2
+    x, logits, wg, wu, wd = _inputs(2, 41, counts)
+    T = x.shape[0]
+    out = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    out = fused_moe(x.cuda(), logits.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), 2, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
+    assert_close(out, fused_moe_forward(x, logits, wg, wu, wd, 2), what="absorbed rows E=150")
 
 
 def test_absorbed_rows_repeatable():

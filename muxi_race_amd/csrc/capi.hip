@@ -154,6 +154,7 @@ int moe_run_prerouted_events(const void* x, const void* w_gate, const void* w_up
   p1.E = (int)E;
   p1.H = H;
   p1.I = I;
+  p1.absorb = 2;  // absorbed rows, pairs kept: few items here (moe_common.h kAbsorbRows)
   // optional stage markers: ev[0] start, [1] stage 1, [2] stage 2
   auto mark = [&](int i) { if (stage_events && stage_events[i]) (void)hipEventRecord((hipEvent_t)stage_events[i], s); };
   mark(0);
@@ -175,6 +176,7 @@ int moe_run_prerouted_events(const void* x, const void* w_gate, const void* w_up
   p2.H = H;
   p2.I = I;
   p2.V = V;
+  p2.absorb = 2;  // as in Stage 1
   rc = check_launch(moe::launch_stage2(p2, 128, moe::kQF16, false, blocks, s), "stage2");
   mark(2);
   return rc;
@@ -370,7 +372,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p1.E = (int)Ee;
   p1.H = H;
   p1.I = I;
-  p1.absorb = 1;  // taken by the instances and expert counts that support it
+  p1.absorb = 1;  // absorbed rows, pairs may become single items (moe_common.h kAbsorbRows)
   if ((rc = check_launch(moe::launch_stage1(p1, (int)bm1, qt, true, rows / bm1, s), "stage1"))) return rc;
   // int8: h (fp16) -> per-row int8 codes + scales, for the routed rows only
   // (sorted id below the sentinel T * ke, row below gpo[E])
@@ -388,7 +390,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.sd = sd;
   p2.out = ws + L.ypair;
   p2.pos = (int32_t*)(ws + L.pos);
-  p2.absorb = 1;  // taken by the instances and expert counts that support it
+  p2.absorb = 1;  // as in Stage 1
   p2.routed = wts;
   p2.routed_f16 = 0;
   p2.gs = gs;

@@ -109,7 +109,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
   // instruction each (those waves wait for one more load per stage).  A wave
   // multiplies them with one of its weight blocks: 1 MFMA per sub-step.
-  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && GATHER && NW == 8 &&
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && NW == 8 &&
                        ((!PAIR && BM == 2 * kBN && S == 2) || (PAIR && BM == kBN && S == 3));
   constexpr int STAGE = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
@@ -125,8 +125,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // gathered (fused) launches follow the align metadata; direct (pre-routed)
   // ones map block -> expert through gidx
   if (GATHER ? !schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w, p.gs,
-                         ABS && p.absorb != 0)
-             : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, kBN, nt, PAIR, w)) return;
+                         ABS ? p.absorb : 0)
+             : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, kBN, nt, PAIR, w, p.gs, p.gpo,
+                            ABS ? p.absorb : 0)) return;
   const int e = w.e;
   if (e < 0) return;  // a block owned by no expert: Stage 2 writes its rows as 0
   const int gpo_e = p.gpo[e];
@@ -179,8 +180,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   const char* asrc = nullptr;
   if (adma) {
     const int r = 8 * wave_id() + (lane_id() >> 3);
-    const int pid = p.sorted_ids[w.ar0 + (r < nar ? r : 0)];
-    asrc = p.x + (int64_t)(pid / p.topk) * kbytes + ((((lane_id() & 7) ^ swz(ROWS + r)) & 7) << 4);
+    const int ra = w.ar0 + (r < nar ? r : 0);  // sorted row
+    const int64_t src_row = GATHER ? p.sorted_ids[ra] / p.topk : ra;
+    asrc = p.x + src_row * kbytes + ((((lane_id() & 7) ^ swz(ROWS + r)) & 7) << 4);
   }
   auto issue_abs = [&](char* stage, int k) {
     if (adma) dma_to_lds<16>(asrc + (size_t)k * kRowBytes, stage + ROWS * kRowBytes + 1024 * wave_id());
@@ -651,7 +653,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // instruction each (those waves wait for one more load per stage).  In a
   // paired item the waves with wm < 2 (one per SIMD) multiply them with one of
   // their two weight blocks; in a single item every wave does.
-  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && FUSED && PAIR && BM == 128 && NW == 8 && S == 3;
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && PAIR && BM == 128 && NW == 8 && S == 3;
   constexpr int SCALES = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;  // fp8: row scales of the step
   constexpr int STAGE = SCALES + (F8 ? 256 * NW : 0);
   static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
@@ -663,8 +665,9 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // fused launches follow the align metadata; pre-routed ones map block ->
   // expert through gidx (every block of the launch is an item)
   if (FUSED ? !schedule(blockIdx.x, p.gpo, p.E, BM, BN, nt, p.host_blocks, false, PAIR, w, p.gs,
-                        ABS && p.absorb != 0)
-            : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, BN, nt, PAIR, w)) return;
+                        ABS ? p.absorb : 0)
+            : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, BN, nt, PAIR, w, p.gs, p.gpo,
+                           ABS ? p.absorb : 0)) return;
   const int row0 = w.row0;
   const int n0 = w.n0;
   const int rx = PAIR ? w.rows : BM;  // token rows of the tile (stage rows [0, rx))
@@ -775,10 +778,21 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   float awr = 0.0f;
   if (ABS && awave) {
     const int m = l & 31;
-    const int pid = p.sorted_ids[w.ar0 + (m < nar ? m : 0)];
-    aorow = (int64_t)go_e + (w.ar0 - gpo_e) + m;
-    awr = m < nar ? reinterpret_cast<const float*>(p.routed)[pid] : 0.0f;
-    if (m < nar && n0 == 0 && wn == 0 && (wm & 1) == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
+    if constexpr (FUSED) {
+      const int pid = p.sorted_ids[w.ar0 + (m < nar ? m : 0)];
+      aorow = (int64_t)go_e + (w.ar0 - gpo_e) + m;
+      awr = m < nar ? reinterpret_cast<const float*>(p.routed)[pid] : 0.0f;
+      if (m < nar && n0 == 0 && wn == 0 && (wm & 1) == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
+    } else {
+      // padded order; raw-order routing weight as for the item's own rows
+      aorow = w.ar0 + m;
+      int64_t ridx = (int64_t)go_e + (w.ar0 - gpo_e) + m;
+      ridx = ridx >= p.V ? p.V - 1 : ridx;
+      ridx = ridx < 0 ? 0 : ridx;
+      if (m < nar && p.V > 0)
+        awr = p.routed_f16 ? (float)reinterpret_cast<const _Float16*>(p.routed)[ridx]
+                           : reinterpret_cast<const float*>(p.routed)[ridx];
+    }
   }
 
   // fp8: the row scales of K step ks (block-major layout, so contiguous) ride
@@ -949,7 +963,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     }
   }
   if constexpr (ABS) {
-    // absorbed rows: their unpadded expert-sorted output rows, stored directly
+    // absorbed rows: stored directly (fused: their unpadded expert-sorted
+    // rows; pre-routed: their padded rows, and the rest of their block as 0)
     if (awave && (l & 31) < nar) {
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
@@ -958,6 +973,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = (_Float16)(aa[4 * rg + q] * awr);
         *reinterpret_cast<f16x4*>(o + aorow * p.H + n) = v;
+      }
+    }
+    if (!FUSED && nar > 0) {
+      for (int idx = threadIdx.x; idx < (BM - nar) * (rw / 8); idx += 64 * NW) {
+        const int r = nar + idx / (rw / 8), c = idx % (rw / 8);
+        *reinterpret_cast<u32x4*>(o + (int64_t)(w.ar0 + r) * p.H + n0 + 8 * c) = u32x4{0, 0, 0, 0};
       }
     }
   }

@@ -38,8 +38,8 @@ struct Stage1Params {
   int64_t I;
   int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher);
                             // direct: blocks of the launch (gidx entries, clamped)
-  int absorb = 0;           // gather, fp16, 256-row or 128-row paired items, E <= 256:
-                            // absorbed rows (moe_common.h)
+  int absorb = 0;           // fp16, 256-row or 128-row paired items, E <= 256: absorbed
+                            // rows; the blocks a pair must keep (moe_common.h), 0: off
 };
 
 // Stage 2: y = h Wd^T, scaled by the routing weight of each row.
@@ -70,7 +70,7 @@ struct Stage2Params {
   int64_t V;                // pre-routed: entries of `routed` (raw index is clamped to V-1)
   int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher);
                             // pre-routed: blocks of the launch (gidx entries, clamped)
-  int absorb = 0;           // fused, fp16, 128-row paired items, E <= 256: absorbed rows
+  int absorb = 0;           // fp16, 128-row paired items, E <= 256: absorbed rows; as in Stage 1
 };
 
 // qt: a QuantType

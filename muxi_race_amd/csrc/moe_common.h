@@ -374,18 +374,25 @@ struct Work {
 // streams anyway.  The item count drops by those blocks' items, and the
 // launch's items are renumbered so that the 8 XCD chunks stay even.  The
 // expert scan keeps 4 values per chunk of 64 experts in registers, so
-// absorption needs E <= kAbsorbMaxE.
+// absorption needs E <= kAbsorbMaxE.  `absorb` is 0 (off) or the blocks of
+// items a paired launch must keep: 1 lets a two-block expert's pair become
+// one full-width item with the rows (fewer, longer items: measured faster in
+// saturated launches, dsv3's Stage 2 1.88 -> 1.82 ms), 2 keeps such pairs
+// (launches of few items, such as the reference's run_kernel cases 1-2,
+// measured slower with fewer items: 0.41 -> 0.43 and 0.73 -> 0.80 ms).
 constexpr int kAbsorbRows = 32;
 constexpr int kAbsorbMaxE = 256;
 
+
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
-                                                  int nt, int host_blocks, bool pair, Work& w);
+                                                  int nt, int host_blocks, bool pair, int absorb, Work& w);
 
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
                                          int nt, int host_blocks, bool tail, bool pair, Work& w,
-                                         const int32_t* __restrict__ gs = nullptr, bool absorb = false) {
-  if (absorb && !tail && E <= kAbsorbMaxE) return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, w);
+                                         const int32_t* __restrict__ gs = nullptr, int absorb = 0) {
+  if (absorb > 0 && !tail && E <= kAbsorbMaxE)
+    return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, absorb, w);
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
   const int total_blocks = tail ? host_blocks : expert_blocks;
@@ -447,7 +454,7 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
 // first item is <= the workgroup's item.
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
-                                                  int nt, int host_blocks, bool pair, Work& w) {
+                                                  int nt, int host_blocks, bool pair, int absorb, Work& w) {
   constexpr int C = kAbsorbMaxE / 64;
   const int l = lane_id();
   int cb0[C], cnb[C], cd[C];
@@ -462,7 +469,8 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
       nb = gpo[e + 1] / BM - b0;
       const int n = gs[e];
       const int v = (n + BM - 1) / BM;  // blocks holding routed rows
-      if (v >= 2 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3) d = nb - (v - 1);
+      if (v >= (pair ? absorb : 1) + 1 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3)
+        d = nb - (v - 1);
     }
     cb0[c] = b0;
     cnb[c] = nb;
@@ -533,8 +541,15 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
 // form a valid paired item for any group metadata: row m of the pair is
 // valid iff m < gs[e] - (row0 - gpo[e]), which is the per-block rule of each
 // half.  A gidx value outside [0, E) gives w.e = -1 (rows owned by no expert).
+//
+// Absorbed rows here keep the numbering: with `absorb` set, a run of two or
+// more blocks whose last block holds 1..kAbsorbRows routed rows (by gs and
+// gpo) gives that block's items nothing to do (they end at once), and the
+// run's first item group takes its rows, as schedule_absorbed describes.
 __device__ __forceinline__ bool schedule_bx(int g, const int32_t* __restrict__ gidx, int nblk, int E, int BM,
-                                            int BN, int nt, bool pair, Work& w) {
+                                            int BN, int nt, bool pair, Work& w,
+                                            const int32_t* __restrict__ gs = nullptr,
+                                            const int32_t* __restrict__ gpo = nullptr, int absorb = 0) {
   const int total = nblk * nt;
   const int per = (total + kNumXcd - 1) / kNumXcd;
   const int slot = g / kNumXcd;
@@ -561,12 +576,18 @@ __device__ __forceinline__ bool schedule_bx(int g, const int32_t* __restrict__ g
     if (m) end = base + (__ffsll((unsigned long long)m) - 1);
   }
   const int nb = end - s;
+  w.e = val >= 0 && val < E ? val : -1;
+  int nm = nb, last = 0;  // blocks with items; routed rows of an absorbed last block
+  if (absorb > 0 && w.e >= 0 && nb >= (pair ? absorb : 1) + 1) {
+    last = gs[w.e] - ((s + nb - 1) * BM - gpo[w.e]);
+    if (last >= 1 && last <= kAbsorbRows) nm = nb - 1;
+  }
   const int local = v - s * nt;
   const int t = local / nb;
   const int r = local % nb;
-  const int P = pair ? nb / 2 : 0;
-  w.e = val >= 0 && val < E ? val : -1;
-  w.shared = pair ? nb > 2 : nb > 1;
+  if (r >= nm) return false;  // the absorbed block's item: its rows ride with the run's first items
+  const int P = pair ? nm / 2 : 0;
+  w.shared = pair ? nm > 2 : nm > 1;
   if (r < 2 * P) {
     w.rows = 2 * BM;
     w.row0 = (s + 2 * (r % P)) * BM;
@@ -577,6 +598,12 @@ __device__ __forceinline__ bool schedule_bx(int g, const int32_t* __restrict__ g
     w.row0 = (s + r) * BM;
     w.bn = BN;
     w.n0 = t * BN;
+  }
+  w.ar0 = 0;
+  w.nar = 0;
+  if (nm < nb && (P > 0 ? (r < 2 * P && r % P == 0) : r == 0)) {
+    w.ar0 = (s + nm) * BM;
+    w.nar = last;
   }
   return true;
 }

@@ -18,7 +18,8 @@ from oracle import fused_moe_forward, route_topk
 pytestmark = pytest.mark.gpu
 
 # per-expert routed rows; with 256-row blocks 257, 288, 513, 543 are absorbed
-# in Stage 1, and with 128-row blocks 257, 288, 513, 543, 160, 385 in Stage 2
+# in Stage 1, and with 128-row blocks 257, 288, 513, 543, 385 and 160 (fused
+# launches let a two-block expert's pair become one item with the rows)
 COUNTS = [257, 288, 289, 545, 513, 543, 256, 1, 0, 33, 160, 161, 385, 417]
 H, I = 256, 256
 
@@ -63,9 +64,10 @@ def test_absorbed_rows_full_output(k, bm):
 
 def test_absorbed_rows_many_experts():
     """E = 150 (the expert scan's third chunk), top-2, the default block_m
-    (128-row padding at ~130 rows per expert): Stage 1 paired 128-row items
-    absorb too.  Experts of 129-160 rows (one block and up to 32 rows) and of
-    257-288 (two blocks and up to 32) next to ones that stay as they are."""
+    (128-row padding at ~140 rows per expert): Stage 1 paired 128-row items
+    absorb too.  Experts of 129-160 rows (one block and up to 32 rows: the pair
+    becomes one item) and of 257-288 (two blocks and up to 32) next to ones
+    that stay as they are."""
     from muxi_race_amd import fused_moe
     rng = np.random.default_rng(5)
     counts = list(COUNTS) + [int(rng.choice([0, rng.integers(1, 40), rng.integers(129, 161), rng.integers(161, 257),
@@ -89,3 +91,26 @@ def test_absorbed_rows_repeatable():
     b = fused_moe(x, logits, wg, wu, wd, 2)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_absorbed_rows_prerouted_padding_zero():
+    """run_kernel keeps its pairs (absorb = 2): runs of three or more blocks
+    whose last block holds <= 32 rows (257, 288, 513, 385 here) are absorbed,
+    129-160-row groups are not.  The absorbed blocks' padding rows must still
+    come back exactly 0 from a NaN-poisoned output, with NaN in x's padding
+    rows (problem_detail.json:50 note 4)."""
+    from _cases import prerouted_inputs
+    from muxi_race_amd import run_kernel
+    from oracle import prerouted_forward
+    sizes = [257, 288, 289, 513, 3, 0, 385, 130, 160]
+    args = list(prerouted_inputs(sizes, 512, 256, seed=77))
+    x, gpo = args[0], args[7].cpu().tolist()
+    pad = torch.ones(x.shape[0], dtype=torch.bool)
+    for e, n in enumerate(sizes):
+        pad[gpo[e]:gpo[e] + n] = False
+    x[pad.to(x.device)] = float("nan")
+    out = torch.full(x.shape, float("nan"), dtype=torch.float16, device=x.device)
+    run_kernel(*args, out)
+    torch.cuda.synchronize()
+    assert_close(out, prerouted_forward(*args), what="prerouted absorbed rows")
+    assert (out[pad.to(out.device)] == 0).all()

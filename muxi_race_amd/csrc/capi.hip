@@ -10,6 +10,12 @@
 
 #include <mutex>
 
+// fp16 Stage 2 over the 256-row padding: 256-row items (1) or 128-row paired
+// items (0).
+#ifndef MOE_S2_F16_256
+#define MOE_S2_F16_256 1
+#endif
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -323,7 +329,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   // padding Stage 2 keeps 128-row (paired) items for fp16 (the 8-bit formats
   // take 256-row ones; see align_bm)
   const int64_t bm1 = block_m;
-  const int64_t bm2 = block_m == 256 && qt == moe::kQF16 ? 128 : block_m;
+  const int64_t bm2 = block_m == 256 && qt == moe::kQF16 && MOE_S2_F16_256 == 0 ? 128 : block_m;
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);

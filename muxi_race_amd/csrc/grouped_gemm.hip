@@ -653,7 +653,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // instruction each (those waves wait for one more load per stage).  In a
   // paired item the waves with wm < 2 (one per SIMD) multiply them with one of
   // their two weight blocks; in a single item every wave does.
-  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && PAIR && BM == 128 && NW == 8 && S == 3;
+  constexpr bool ABS = MOE_ABSORB != 0 && !I8 && NW == 8 &&
+                       ((PAIR && BM == 128 && S == 3) || (!PAIR && BM == 256 && S == 2));
   constexpr int SCALES = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;  // fp8: row scales of the step
   constexpr int STAGE = SCALES + (F8 ? 256 * NW : 0);
   static_assert(!PAIR || (BN == 2 * BM && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
@@ -770,10 +771,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   for (int a = 0; a < L::NBN; ++a)
 #pragma unroll
     for (int b = 0; b < L::NBM; ++b) acc[a][b] = Acc{};
-  // absorbed rows x weight block (wm & 1) of this wave; their pair, output
+  // absorbed rows x weight block aj of this wave (256-row items: block wm of
+  // its four; 128-row items: block wm & 1 of its two); their pair, output
   // row and routing weight (lane l: absorbed row l % 32)
   f32x16 aa = {};
-  const int awr0 = wr0 + 32 * (wm & 1);
+  const int aj = L::NBN >= 4 ? wm : (wm & 1);
+  const int awr0 = wr0 + 32 * aj;
   int64_t aorow = 0;
   float awr = 0.0f;
   if (ABS && awave) {
@@ -782,7 +785,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       const int pid = p.sorted_ids[w.ar0 + (m < nar ? m : 0)];
       aorow = (int64_t)go_e + (w.ar0 - gpo_e) + m;
       awr = m < nar ? reinterpret_cast<const float*>(p.routed)[pid] : 0.0f;
-      if (m < nar && n0 == 0 && wn == 0 && (wm & 1) == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
+      if (m < nar && n0 == 0 && wn == 0 && aj == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
     } else {
       // padded order; raw-order routing weight as for the item's own rows
       aorow = w.ar0 + m;
@@ -968,7 +971,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     if (awave && (l & 31) < nar) {
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
-        const int n = n0 + wn * L::WTN + 32 * (wm & 1) + 8 * rg + 4 * (l >> 5);
+        const int n = n0 + wn * L::WTN + 32 * aj + 8 * rg + 4 * (l >> 5);
         f16x4 v;
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = (_Float16)(aa[4 * rg + q] * awr);
@@ -1136,9 +1139,11 @@ hipError_t launch_stage2(const Stage2Params& params, int block_m, int qt, bool f
       if (qt == kQF8) return go2_128<kQF8, true>(p, mb, s);
       return go2_128<kQF16, true>(p, mb, s);
     case 256:
-      // 8-bit, 256 token rows x 256 weight rows: two 64 KiB stages
+      // 256 token rows x 256 weight rows: two 64 KiB stages (fp16: with the
+      // absorbed rows, two 68 KiB stages)
       if (qt == kQF8 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQF8, true, false>(p, mb, s);
       if (qt == kQI8 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQI8, true, false>(p, mb, s);
+      if (qt == kQF16 && p.H % 256 == 0) return go2<256, 4, 256, 8, kQF16, true, false>(p, mb, s);
       return hipErrorInvalidValue;
   }
   return hipErrorInvalidValue;

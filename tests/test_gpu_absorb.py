@@ -114,3 +114,22 @@ def test_absorbed_rows_prerouted_padding_zero():
     torch.cuda.synchronize()
     assert_close(out, prerouted_forward(*args), what="prerouted absorbed rows")
     assert (out[pad.to(out.device)] == 0).all()
+
+
+def test_absorbed_rows_256_row_items_many_experts():
+    """E = 80 at ~270 rows per expert (block_m 0 picks the 256-row padding):
+    both stages on 256-row items, with the expert scan over two chunks.
+    Experts of 257-288 and 513-544 rows are absorbed, 289+ and 545+ are not."""
+    from muxi_race_amd import fused_moe
+    rng = np.random.default_rng(9)
+    counts = [int(rng.choice([rng.integers(257, 289), rng.integers(289, 400), rng.integers(513, 545),
+                              rng.integers(100, 256), 0])) for _ in range(80)]
+    counts[-1] += sum(counts) % 2
+    assert sum(counts) / len(counts) >= 192
+    x, logits, wg, wu, wd = _inputs(2, 43, counts)
+    T = x.shape[0]
+    out = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    out = fused_moe(x.cuda(), logits.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), 2, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
+    assert_close(out, fused_moe_forward(x, logits, wg, wu, wd, 2), what="absorbed rows E=80, 256-row items")

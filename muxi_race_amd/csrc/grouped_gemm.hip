@@ -103,7 +103,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using L = Layout<BM, WAVES_M, kBN, NW>;
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + 2 * kBN;
-  using LD = DmaTile<ROWS, NW>;
+  using LD = DmaTile<ROWS, NW, !I8 && S == 2>;  // weight rows first on the fp16 two-stage ring
   // Absorbed rows (fp16, gathered; 256-row items on the two-stage ring and
   // 128-row paired items on the three-stage one): kAbsorbRows more token rows
   // at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   // one scale per row, applied in the epilogue); fp16 / fp8: fp32
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + BN;
-  using LD = DmaTile<ROWS, NW>;
+  using LD = DmaTile<ROWS, NW, !I8 && S == 2>;  // weight rows first on the fp16 two-stage ring
   // Absorbed rows (fp16 fused 128-row paired items): kAbsorbRows more token
   // rows at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
   // instruction each (those waves wait for one more load per stage).  In a

@@ -157,7 +157,7 @@ __device__ __forceinline__ void dma_to_lds(const void* g, void* lds) {
 // logical chunk (l%8) ^ swz(r), so lane l loads that chunk of its row; the 8
 // lanes of a row still cover its 128 contiguous bytes.  Wave w issues the
 // instructions for row groups NW*i + w.
-template <int ROWS, int NW>
+template <int ROWS, int NW, bool WEIGHTS_FIRST = false>
 struct DmaTile {
   static constexpr int NI = ROWS / (8 * NW);  // instructions per wave per K step
   static_assert(NI >= 1 && ROWS == 8 * NW * NI, "tile rows must be a multiple of 8 * waves");
@@ -169,18 +169,30 @@ struct DmaTile {
     const int l = lane_id();
     src[i] = rowp + (((l & 7) ^ swz(row_of(i))) << 4);
   }
+  // WEIGHTS_FIRST: instructions go out last row group first.  A stage holds
+  // token rows, then weight rows; the weight rows (HBM misses) are its long
+  // pole and the token rows (L2 hits) its short one.  Measured per kernel:
+  // the fp16 two-stage rings (mixtral's Stage 1 1.000 -> 0.982 ms, Stage 2
+  // 0.495 -> 0.482 ms) take it; the 8-bit 256-row Stage 2 (+2.5%) and the
+  // three-stage rings with their spread issue (dsv3 Stage 2 +1%) do not.
+  __device__ __forceinline__ static constexpr int order(int j) { return WEIGHTS_FIRST ? NI - 1 - j : j; }
   __device__ __forceinline__ void issue(char* lds, int ks) const {
     const int w = wave_id();
 #pragma unroll
-    for (int i = 0; i < NI; ++i) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+    for (int j = 0; j < NI; ++j) {
+      const int i = order(j);
+      dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+    }
   }
   // The instructions i with i % PARTS == part of issue(lds, ks).
   template <int PARTS>
   __device__ __forceinline__ void issue_part(char* lds, int ks, int part) const {
     const int w = wave_id();
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-      if (i % PARTS == part) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+    for (int j = 0; j < NI; ++j) {
+      const int i = order(j);
+      if (j % PARTS == part) dma_to_lds<16>(src[i] + (size_t)ks * kRowBytes, lds + 1024 * (NW * i + w));
+    }
   }
   // As issue(), with tile rows from `weights_from` on loaded under the
   // streaming weight policy (kNoStream: none); an instruction's 8 rows never

@@ -133,3 +133,37 @@ def test_absorbed_rows_256_row_items_many_experts():
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
     assert_close(out, fused_moe_forward(x, logits, wg, wu, wd, 2), what="absorbed rows E=80, 256-row items")
+
+
+@pytest.mark.parametrize("bm", [0, 128])
+def test_last_blocks_beyond_absorption(bm):
+    """Last blocks of 33-64 rows stay items of their own (absorption takes at
+    most 32 rows; splitting 33-64 over two item groups measured slower at
+    dsv3) next to absorbed and plain experts: 424, 572, 562, 296, 600 and
+    others, top-1, the 256-row (bm 0) and 128-row paddings; pre-routed too,
+    with NaN-poisoned padding."""
+    from muxi_race_amd import fused_moe
+    counts = [424, 572, 562, 296, 600, 250, 0, 31, 200]
+    x, logits, wg, wu, wd = _inputs(1, 44, counts)
+    T = x.shape[0]
+    out = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    out = fused_moe(x.cuda(), logits.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), 1, block_m=bm, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite values left in the NaN-poisoned output"
+    assert_close(out, fused_moe_forward(x, logits, wg, wu, wd, 1), what=f"last blocks of 33-64 rows bm={bm}")
+    if bm == 128:
+        from _cases import prerouted_inputs
+        from muxi_race_amd import run_kernel
+        from oracle import prerouted_forward
+        sizes = [424, 572, 296, 3, 0, 562]
+        args = list(prerouted_inputs(sizes, 512, 256, seed=45))
+        xp, gpo = args[0], args[7].cpu().tolist()
+        pad = torch.ones(xp.shape[0], dtype=torch.bool)
+        for e, n in enumerate(sizes):
+            pad[gpo[e]:gpo[e] + n] = False
+        xp[pad.to(xp.device)] = float("nan")
+        o = torch.full(xp.shape, float("nan"), dtype=torch.float16, device=xp.device)
+        run_kernel(*args, o)
+        torch.cuda.synchronize()
+        assert_close(o, prerouted_forward(*args), what="prerouted last blocks of 33-64 rows")
+        assert (o[pad.to(o.device)] == 0).all()

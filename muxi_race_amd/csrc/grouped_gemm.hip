@@ -29,8 +29,8 @@
 #endif
 // Stage 1 8-bit 256-row items on the split ring (1) or on two whole 64 KiB
 // stages (0).
-// Absorbed rows (see schedule_absorbed): fp16 256-row Stage 1 items and
-// 128-row paired Stage 2 items take an expert's last few rows instead of
+// Absorbed rows (see schedule_absorbed): fp16 256-row items and 128-row
+// paired items of both stages take an expert's last few rows instead of
 // giving them items of their own; 0 turns it off.
 #ifndef MOE_ABSORB
 #define MOE_ABSORB 1
@@ -104,8 +104,8 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + 2 * kBN;
   using LD = DmaTile<ROWS, NW, !I8 && S == 2>;  // weight rows first on the fp16 two-stage ring
-  // Absorbed rows (fp16, gathered; 256-row items on the two-stage ring and
-  // 128-row paired items on the three-stage one): kAbsorbRows more token rows
+  // Absorbed rows (fp16; 256-row items on the two-stage ring and 128-row
+  // paired items on the three-stage one): kAbsorbRows more token rows
   // at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
   // instruction each (those waves wait for one more load per stage).  A wave
   // multiplies them with one of its weight blocks: 1 MFMA per sub-step.
@@ -648,11 +648,12 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
   using Acc = typename std::conditional<I8 && !F8, i32x16, f32x16>::type;
   constexpr int ROWS = BM + BN;
   using LD = DmaTile<ROWS, NW, !I8 && S == 2>;  // weight rows first on the fp16 two-stage ring
-  // Absorbed rows (fp16 fused 128-row paired items): kAbsorbRows more token
-  // rows at stage rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row
-  // instruction each (those waves wait for one more load per stage).  In a
-  // paired item the waves with wm < 2 (one per SIMD) multiply them with one of
-  // their two weight blocks; in a single item every wave does.
+  // Absorbed rows (fp16; 128-row paired items on the three-stage ring and
+  // 256-row items on the two-stage one): kAbsorbRows more token rows at stage
+  // rows [ROWS, ROWS + 32), loaded by waves 0-3 with one 8-row instruction
+  // each (those waves wait for one more load per stage).  In a paired item
+  // the waves with wm < 2 (one per SIMD) multiply them with one of their two
+  // weight blocks; in a single or 256-row item every wave does.
   constexpr bool ABS = MOE_ABSORB != 0 && !I8 && NW == 8 &&
                        ((PAIR && BM == 128 && S == 3) || (!PAIR && BM == 256 && S == 2));
   constexpr int SCALES = (ROWS + (ABS ? kAbsorbRows : 0)) * kRowBytes;  // fp8: row scales of the step

@@ -147,3 +147,28 @@ def scale_contrast_case(fmt_q):
     ref = fused_moe_forward(x, lg, wg, wu, wd, k).float()
     q = [fmt_q(w) for w in (wg, wu, wd)]
     return x, lg, wg, wu, wd, ref, q, k
+
+
+def exact_routing_inputs(k, seed, counts, H, I):
+    """CPU x, logits and weights whose top-k routing gives expert e exactly
+    counts[e] pairs (with k > 1 the k experts of a token differ)."""
+    from oracle import route_topk
+    g = torch.Generator().manual_seed(seed)
+    E = len(counts)
+    slots = np.repeat(np.arange(E), counts)  # expert-sorted pair slots
+    P = len(slots)
+    assert P % k == 0 and max(counts) < P // k
+    T = P // k
+    logits = torch.randn(T, E, generator=g) * 0.1
+    perm = torch.randperm(T, generator=g).numpy()  # tokens in random order
+    for j in range(k):
+        # token perm[i] takes slot i + j*T: an expert's run is shorter than T,
+        # so the k slots of a token name k different experts
+        logits[perm, torch.from_numpy(slots[j * T:(j + 1) * T])] += 8.0 - j
+    x = torch.randn(T, H, generator=g).half()
+    wg = (torch.randn(E, I, H, generator=g) * 0.05).half()
+    wu = (torch.randn(E, I, H, generator=g) * 0.05).half()
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).half()
+    ids, _ = route_topk(logits.numpy(), k, None)
+    np.testing.assert_array_equal(np.bincount(ids.ravel(), minlength=E), counts)
+    return x, logits, wg, wu, wd

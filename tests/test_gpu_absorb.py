@@ -1,8 +1,8 @@
 """GPU parity of absorbed rows.  When an expert's last block holds at most 32
 routed rows (after at least one other block), the schedule gives that block
 no items: the expert's first item group takes those rows as extra token rows
-(moe_common.h schedule_absorbed; fp16 Stage 1 256-row items and Stage 2
-128-row paired items, E <= 64).  Exact per-expert counts straddle the rule:
+(moe_common.h schedule_absorbed; fp16 256-row items and 128-row paired
+items of both stages, E <= 256).  Exact per-expert counts straddle the rule:
 1 and 32 rows past a block boundary are absorbed, 33 are not, and so are
 single-block experts, empty ones and exact multiples.  They run under the
 256-row padding (block_m 0 picks it here: H % 256 == 0, >= 192 rows per
@@ -12,8 +12,9 @@ import numpy as np
 import pytest
 import torch
 
+from _cases import exact_routing_inputs
 from conftest import assert_close
-from oracle import fused_moe_forward, route_topk
+from oracle import fused_moe_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -25,27 +26,7 @@ H, I = 256, 256
 
 
 def _inputs(k, seed, counts=COUNTS):
-    """x, logits and weights whose top-k routing gives expert e exactly
-    counts[e] pairs (k = 2: the two experts of a token differ)."""
-    g = torch.Generator().manual_seed(seed)
-    E = len(counts)
-    slots = np.repeat(np.arange(E), counts)  # expert-sorted pair slots
-    P = len(slots)
-    assert P % k == 0 and max(counts) < P // k
-    T = P // k
-    logits = torch.randn(T, E, generator=g) * 0.1
-    perm = torch.randperm(T, generator=g).numpy()  # tokens in random order
-    for j in range(k):
-        # token perm[i] takes slot i + j*T: an expert's run is shorter than T,
-        # so the k slots of a token name k different experts
-        logits[perm, torch.from_numpy(slots[j * T:(j + 1) * T])] += 8.0 - j
-    x = torch.randn(T, H, generator=g).half()
-    wg = (torch.randn(E, I, H, generator=g) * 0.05).half()
-    wu = (torch.randn(E, I, H, generator=g) * 0.05).half()
-    wd = (torch.randn(E, H, I, generator=g) * 0.05).half()
-    ids, _ = route_topk(logits.numpy(), k, None)
-    np.testing.assert_array_equal(np.bincount(ids.ravel(), minlength=E), counts)
-    return x, logits, wg, wu, wd
+    return exact_routing_inputs(k, seed, counts, H, I)
 
 
 @pytest.mark.parametrize("k", [1, 2])

@@ -125,6 +125,10 @@ def _random_case(T, H, I, E, k, seed, bias=True):
     (3, 128, 256, 1024, 32),    # widest routing: E = 1024 experts, k = 32 choices
     (257, 256, 128, 32, 32),    # every token takes every expert (k = E)
     (129, 384, 640, 5, 3),      # odd expert count, H and I not powers of two
+    # more than 256 experts (no absorbed rows): ~109 rows each on paired
+    # 128-row items, and ~218 each on 256-row items (H a multiple of 256)
+    (4096, 128, 256, 300, 8),
+    (8192, 256, 256, 300, 8),
 ])
 def test_extreme_shapes(T, H, I, E, k):
     _check(_random_case(T, H, I, E, k, T + E), what=f"T={T} H={H} I={I} E={E} k={k}")

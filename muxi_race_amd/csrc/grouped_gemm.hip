@@ -6,11 +6,18 @@
 // Reference algorithm: 初审材料/源代码/submission.py Stage1 family (:136-247,
 // :1391-1635) and Stage2 family (:655-795, :1132-1378); base form
 // xpuoj_data/submission.py:31-129 and :253-331.  The tiling here is this
-// build's own.  A workgroup (4 waves for 32/64-row tiles, 8 for 128-row ones)
-// computes a BM x 128 output tile (Stage 1: gate and up at once, sharing the
-// token tile; Stage 2 of 128-row tiles: 256 features), or a paired 2*BM x 64
-// (x 128) item for experts with several blocks.  K advances 128 bytes per step
-// through an S-stage ring of XOR-swizzled LDS tiles filled by direct
+// build's own.  One workgroup per item:
+//   - 32- and 64-row tiles (4 waves) for decode-sized batches; fp16 Stage 1 of
+//     32-row tiles runs the narrow kernel (32 gate + 32 up features per item);
+//   - 128-row tiles (8 waves): BM rows x 256 weight rows (Stage 1: 128 gate +
+//     128 up, sharing the token tile; Stage 2: 256 features), or a paired item
+//     of 2*BM rows x 128 weight rows for two blocks of one expert, which
+//     streams their weight tile once;
+//   - 256-row tiles (8 waves) when experts average >= 192 rows: two 64 KiB
+//     stages, or the split ring below for 8-bit Stage 1;
+// and an expert's last block of at most 32 rows rides with its first item
+// group (absorbed rows, moe_common.h schedule_absorbed).  K advances 128 bytes
+// per step through an S-stage ring of XOR-swizzled LDS tiles filled by direct
 // global->LDS loads (global_load_lds_dwordx4), so S-2 steps of loads stay in
 // flight behind the MFMAs of the current step, with one barrier per step.
 #include "launch.h"

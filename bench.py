@@ -378,62 +378,6 @@ def calib_copy(dev):
     return gbs
 
 
-def probe_ring(dev, reps=5):
-    """The load-path probe (muxi_race_amd/libmoe_probe.so, csrc/probe/ring_probe.hip):
-    tile rows streamed through the stages' direct-to-LDS ring with no compute,
-    for the two ring shapes of the GEMM kernels, two row pitches (Stage 1's
-    H = 7168 and Stage 2's I = 2048 fp16 rows), shares of L2-hit rows and the
-    two cache policies.  Returns a list of rows with the streamed (miss) rate
-    and the LDS fill rate in TB/s; nothing of the operator library is used."""
-    import torch
-    plib = ctypes.CDLL(os.path.join(ROOT, "muxi_race_amd", "libmoe_probe.so"))
-    fn = plib.moe_probe_ring
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
-                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    # (variant, rows, ring, workgroups): 1 workgroup per CU for the 144 KiB
-    # ring, 2 for the 72 KiB one; 4 rounds of the chip either way
-    shapes = {0: (384, "384 rows (128 + 256 or 256 + 128), 3 stages, 8 waves", 1024),
-              2: (96, "96 rows (32 + 64), 6 stages, 4 waves", 2048),
-              4: (512, "512 rows (256 + 256), 2 stages, 8 waves", 1024),
-              6: (384, "384 rows, 3 stages, 8 waves; hit rows issued by waves 0-3, streamed rows by 4-7", 1024)}
-    cases = [(0, 14336, h) for h in (0, 128, 256, 320, 384)] + [(0, 4096, h) for h in (0, 128, 256, 320, 384)] + \
-            [(1, 14336, h) for h in (0, 128, 256, 320)] + [(1, 4096, h) for h in (0, 128, 256, 320)] + [
-             (2, 14336, 0), (3, 14336, 0), (2, 4096, 0), (3, 4096, 0)] + \
-            [(4, p, h) for p in (14336, 4096) for h in (0, 256)] + \
-            [(v, p, h) for p in (14336, 4096) for v, h in ((6, 128), (7, 256))]
-    need = max(shapes[v & 6][2] * shapes[v & 6][0] * p for v, p, _ in cases)
-    buf = torch.zeros(need, dtype=torch.uint8, device=dev)
-    hit = torch.zeros(512 * 14336, dtype=torch.uint8, device=dev)
-    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    out = []
-    for v, pitch, hr in cases:
-        rows, shape, groups = shapes[v & 6]
-        nk = pitch // 128
-        call = lambda: fn(v, buf.data_ptr(), need, hit.data_ptr(), hit.numel(), pitch, nk, hr, groups,
-                          sink.data_ptr(), stream)
-        for _ in range(2):
-            rc = call()
-            if rc:
-                raise RuntimeError(f"moe_probe_ring({v}, pitch {pitch}, hit rows {hr}) returned {rc}")
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record()
-        for _ in range(reps):
-            call()
-        b.record()
-        torch.cuda.synchronize()
-        sec = a.elapsed_time(b) / reps * 1e-3
-        step_bytes = groups * nk * 128
-        out.append(dict(ring=shape, row_pitch=pitch, hit_rows=hr, policy="non-temporal" if v & 1 and v < 6 else "default",
-                        us=round(sec * 1e6, 1), streamed_tb_per_s=round(step_bytes * (rows - hr) / sec / 1e12, 2),
-                        lds_fill_tb_per_s=round(step_bytes * rows / sec / 1e12, 2)))
-        print(f"probe {out[-1]}", file=sys.stderr, flush=True)
-    del buf, hit, sink
-    return out
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -471,9 +415,6 @@ def main():
                          "(e.g. 128: one block per expert, 256: pairs); implies --no-extra")
     ap.add_argument("--only", choices=("prerouted", "configs"), default=None,
                     help="run only that extra leg (for profiling), printing its JSON")
-    ap.add_argument("--probe-ring", action="store_true",
-                    help="run only the load-path probe (libmoe_probe.so: rows streamed through the stages' "
-                         "direct-to-LDS ring, no compute) and print its table as one JSON line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (3x) as the byte-counter calibration "
                          "kernel for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -490,9 +431,6 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.probe_ring:
-        print(json.dumps({"probe_ring": probe_ring(dev)}), flush=True)
-        return
     if args.only is not None:
         leg = bench_prerouted(lib(), dev, args.steps, args.warmup, not args.no_check) if args.only == "prerouted" \
             else run_configs(lib(), dev, args.steps, args.warmup, None)

@@ -83,23 +83,5 @@ def build(verbose: bool = False, defines: dict | None = None, out: Path | None =
     return lib
 
 
-PROBE_SRC = CSRC / "probe" / "ring_probe.hip"
-PROBE_LIB = PKG / "libmoe_probe.so"
-
-
-def build_probe() -> Path:
-    """Compile the load-path probe (csrc/probe/ring_probe.hip, measurement
-    only) into muxi_race_amd/libmoe_probe.so; returns its path."""
-    OBJDIR.mkdir(parents=True, exist_ok=True)
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [_hipcc(), *HIP_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
-
-
 if __name__ == "__main__":
     print(build(verbose=True))
-    print(build_probe())

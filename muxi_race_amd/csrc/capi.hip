@@ -84,10 +84,11 @@ int64_t pick_bm(int64_t T, int64_t E, int64_t k) {
 // Rows per block of the align padding.  block_m != 0 is the caller's choice,
 // used by both stages.  0: pick_bm's size, except that 128 becomes 256 when
 // experts hold >= 192 routed rows on average and H is a multiple of 256: then
-// Stage 1 runs 256-row items (and so does fp8's Stage 2), measured faster on
-// every format.  A stage that keeps 128-row items runs them over the same
-// padding; those that fall in a block's empty second half end at once.  At
-// fewer rows per expert half-empty 256-row blocks cost more than they save.
+// both stages run 256-row items for every format, measured faster on each.
+// (Built with MOE_S2_F16_256=0, fp16 Stage 2 keeps 128-row paired items over
+// the 256-row padding; those that fall in a block's empty second half end at
+// once.)  At fewer rows per expert half-empty 256-row blocks cost more than
+// they save.
 int64_t align_bm(int64_t T, int64_t E, int64_t k, int64_t H, int64_t block_m) {
   if (block_m) return block_m;
   const int64_t bm = pick_bm(T, E, k);
@@ -325,9 +326,9 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   const FusedLayout L = fused_layout(T, H, I, Ee, ke, block_m, qt);
   const int64_t need = L.total + router_ws;
   if (workspace_bytes < need) return fail(MOE_ERR_WORKSPACE, "workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
-  // rows per item of each stage: block_m, except that over the 256-row
-  // padding Stage 2 keeps 128-row (paired) items for fp16 (the 8-bit formats
-  // take 256-row ones; see align_bm)
+  // rows per item of each stage: block_m for both stages and every format
+  // (over the 256-row padding, 256-row items), unless built with
+  // MOE_S2_F16_256=0, where fp16 Stage 2 keeps 128-row paired items there
   const int64_t bm1 = block_m;
   const int64_t bm2 = block_m == 256 && qt == moe::kQF16 && MOE_S2_F16_256 == 0 ? 128 : block_m;
   hipStream_t s = (hipStream_t)stream;

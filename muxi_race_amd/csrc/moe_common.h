@@ -116,10 +116,9 @@ __device__ __forceinline__ void barrier_no_fence() {
 // Cache policy of weight loads that no other tile repeats, used by the
 // decode-sized (32-row) kernels.  A weight tile read by exactly one item is
 // loaded non-temporal (the gfx950 `nt` bit, cache-policy immediate 2):
-// measured with the load-path probe (csrc/probe/ring_probe.hip, the 96-row
-// decode ring), streaming reads rise from 6.15 to 7.12 TB/s (rows 14 KiB
-// apart) and from 5.45 to 6.14 TB/s (4 KiB apart), and decode from 0.575 to
-// 0.533 ms.  Weight tiles that sibling items of a multi-block
+// decode went from 0.575 to 0.533 ms with it (a load-only copy of the 96-row
+// decode ring streamed 6.15 -> 7.12 TB/s at rows 14 KiB apart, 5.45 -> 6.14
+// TB/s at 4 KiB).  Weight tiles that sibling items of a multi-block
 // expert re-read from L2, and token / intermediate rows, keep the default
 // policy (non-temporal there measured slower: fewer L2 hits); the wide-tile
 // kernels load everything with the default policy (no gain measured there,
@@ -310,8 +309,7 @@ __device__ __forceinline__ int quant_i8(float x, float inv) {
 // Its codes equal a bit-level restatement of the format -- the fp32 mantissa
 // rounded to 3 bits with the carry running into the rebiased exponent, and
 // below 2^-6 the round-to-even multiple of 2^-9 -- for every float of
-// magnitude <= 448 (the load-path probe library's moe_probe_f8_encoder,
-// run by the fp8 GPU tests).
+// magnitude <= 448 (checked exhaustively by the fp8 GPU tests).
 __device__ __forceinline__ float f8_clamp(float v) { return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f); }
 __device__ __forceinline__ uint32_t f8_e4m3(float v) {
   const float c = f8_clamp(v);

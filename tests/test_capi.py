@@ -123,23 +123,3 @@ def test_256_row_padding_policy():
         assert ws(4096, 7168, 2048, 256, 8, 0, f) == ws(4096, 7168, 2048, 256, 8, 128, f)
     # H not a multiple of 256: no padding
     assert ws(2048, 4224, 14336, 8, 2, 0, 0) == ws(2048, 4224, 14336, 8, 2, 128, 0)
-
-
-def test_probe_library_rejects_bad_arguments_without_gpu():
-    """The load-path probe (libmoe_probe.so, measurement only) validates its
-    arguments on the host: bad ones return -1 before any launch."""
-    path = ROOT / "muxi_race_amd" / "libmoe_probe.so"
-    if not path.exists():
-        pytest.skip("libmoe_probe.so not built")
-    fn = ctypes.CDLL(str(path)).moe_probe_ring
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
-                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    buf = ctypes.create_string_buffer(64)
-    p = ctypes.cast(buf, ctypes.c_void_p)
-    assert fn(99, p, 1 << 40, p, 1 << 40, 4096, 32, 0, 1, p, None) == -1         # no such variant
-    assert fn(0, p, 1 << 40, p, 1 << 40, 4096, 33, 0, 1, p, None) == -1          # K past the row
-    assert fn(0, p, 1 << 40, p, 1 << 40, 4096, 32, 12, 1, p, None) == -1         # hit rows not a multiple of 8
-    assert fn(0, p, 1000, p, 1 << 40, 4096, 32, 0, 1, p, None) == -1             # stream region too small
-    assert fn(0, p, 1 << 40, p, 100, 4096, 32, 8, 1, p, None) == -1              # hit region too small
-    assert fn(2, p, 1 << 40, p, 1 << 40, 4096, 32, 104, 1, p, None) == -1        # more hit rows than the ring

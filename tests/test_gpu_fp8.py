@@ -150,11 +150,11 @@ def test_fp8_encoder_matches_the_format_for_every_float():
     """The kernels' e4m3 encoder (the gfx950 conversion instruction, one and
     four codes at a time) against a bit-level restatement of the format with
     round to nearest even, over every float of magnitude <= 448 -- all the
-    values the quantisers feed it (libmoe_probe.so's moe_probe_f8_encoder)."""
+    values the quantisers feed it (tests/f8_encoder_check.hip, built into
+    tests/libf8check.so by tests/_native.py)."""
     import ctypes
-    from pathlib import Path
-    path = Path(__file__).resolve().parents[1] / "muxi_race_amd" / "libmoe_probe.so"
-    fn = ctypes.CDLL(str(path)).moe_probe_f8_encoder
+    from _native import build_f8check
+    fn = ctypes.CDLL(str(build_f8check())).f8_encoder_check
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     cnt = torch.zeros(2, dtype=torch.int64, device="cuda")

@@ -395,7 +395,8 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.as_stride = rows;
   p2.wd = (const char*)wd;
   p2.sd = sd;
-  p2.out = ws + L.ypair;
+  p2.out = MOE_S2_SCATTER ? (char*)out : ws + L.ypair;
+  p2.topk = (int)ke;
   p2.pos = (int32_t*)(ws + L.pos);
   p2.absorb = 1;  // as in Stage 1
   p2.routed = wts;
@@ -411,8 +412,13 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.E = (int)Ee;
   p2.H = H;
   p2.I = I;
+  if (MOE_S2_SCATTER && (rc = check_launch(moe::launch_zero(out, T * H * 2, s), "zero_out"))) return rc;
   if ((rc = check_launch(moe::launch_stage2(p2, (int)bm2, qt, true, rows / bm2, s), "stage2"))) return rc;
   mark(5);
+  if (MOE_S2_SCATTER) {  // Stage 2 added every pair row into `out`
+    mark(6);
+    return MOE_OK;
+  }
   rc = check_launch(moe::launch_combine(ws + L.ypair, (const int32_t*)(ws + L.pos), T, H, (int)ke, out, s,
                                         shard ? ids : nullptr, (int)e_begin, (int)E),
                     "combine");

@@ -53,6 +53,20 @@
 
 namespace moe {
 
+// out[0..3] += v (two packed fp16 atomic adds; no return value)
+__device__ __forceinline__ void atomic_add_f16x4(_Float16* out, f16x4 v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(1))) h2 GlobalH2;
+  GlobalH2* p = (GlobalH2*)(uintptr_t)out;
+  __builtin_amdgcn_global_atomic_fadd_v2f16(p, h2{v[0], v[1]});
+  __builtin_amdgcn_global_atomic_fadd_v2f16(p + 1, h2{v[2], v[3]});
+#else
+  (void)out;
+  (void)v;
+#endif
+}
+
 template <int BM, int WAVES_M, int BN, int NW>
 struct Layout {
   static constexpr int WAVES_N = NW / WAVES_M;
@@ -753,7 +767,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
       // the pair's output row: its unpadded position in the expert-sorted
       // order, so an item writes one contiguous run of rows; the combine
       // finds it through pos[pair], written here once per row
-      orow[b] = (int64_t)go_e + (row0 - gpo_e) + xr0 + 32 * b + (l & 31);
+      orow[b] = MOE_S2_SCATTER ? (int64_t)(valid ? pid[b] / p.topk : 0)
+                               : (int64_t)go_e + (row0 - gpo_e) + xr0 + 32 * b + (l & 31);
       wr[b] = reinterpret_cast<const float*>(p.routed)[valid ? pid[b] : 0];
       if (valid && n0 == 0 && wn == 0 && l < 32) p.pos[pid[b]] = (int32_t)orow[b];
       if constexpr (I8 && !F8) shv[b] = valid ? p.a_scale[row0 + xr0 + 32 * b + (l & 31)] : 0.0f;
@@ -791,7 +806,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     const int m = l & 31;
     if constexpr (FUSED) {
       const int pid = p.sorted_ids[w.ar0 + (m < nar ? m : 0)];
-      aorow = (int64_t)go_e + (w.ar0 - gpo_e) + m;
+      aorow = MOE_S2_SCATTER ? (int64_t)(pid / p.topk) : (int64_t)go_e + (w.ar0 - gpo_e) + m;
       awr = m < nar ? reinterpret_cast<const float*>(p.routed)[pid] : 0.0f;
       if (m < nar && n0 == 0 && wn == 0 && aj == 0 && l < 32) p.pos[pid] = (int32_t)aorow;
     } else {
@@ -957,6 +972,7 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
         }
         if constexpr (kStaged)
           *reinterpret_cast<f16x4*>(smem + m * pitch + 16 * ((nl >> 3) ^ (m & xm)) + 2 * (nl & 7)) = v;
+        else if constexpr (FUSED && MOE_S2_SCATTER) atomic_add_f16x4(o + orow[b] * p.H + n, v);
         else *reinterpret_cast<f16x4*>(o + orow[b] * p.H + n) = v;
       }
   }
@@ -968,9 +984,15 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
     const int rows_out = FUSED ? actual : rx;
     for (int idx = threadIdx.x; idx < rows_out << shift; idx += 64 * NW) {
       const int r = idx >> shift, c = idx & ((1 << shift) - 1);
-      const int64_t orr = FUSED ? (int64_t)go_e + (row0 - gpo_e) + r : (int64_t)(row0 + r);
-      *reinterpret_cast<u32x4*>(o + orr * p.H + n0 + 8 * c) =
-          *reinterpret_cast<const u32x4*>(smem + r * pitch + 16 * (c ^ (r & xm)));
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * pitch + 16 * (c ^ (r & xm)));
+      if constexpr (FUSED && MOE_S2_SCATTER) {
+        _Float16* dst = o + (int64_t)(p.sorted_ids[row0 + r] / p.topk) * p.H + n0 + 8 * c;
+        atomic_add_f16x4(dst, __builtin_bit_cast(f16x4, u32x2{v[0], v[1]}));
+        atomic_add_f16x4(dst + 4, __builtin_bit_cast(f16x4, u32x2{v[2], v[3]}));
+      } else {
+        const int64_t orr = FUSED ? (int64_t)go_e + (row0 - gpo_e) + r : (int64_t)(row0 + r);
+        *reinterpret_cast<u32x4*>(o + orr * p.H + n0 + 8 * c) = v;
+      }
     }
   }
   if constexpr (ABS) {
@@ -983,7 +1005,8 @@ __global__ __launch_bounds__(64 * NW) void stage2_kernel(Stage2Params p) {
         f16x4 v;
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = (_Float16)(aa[4 * rg + q] * awr);
-        *reinterpret_cast<f16x4*>(o + aorow * p.H + n) = v;
+        if constexpr (FUSED && MOE_S2_SCATTER) atomic_add_f16x4(o + aorow * p.H + n, v);
+        else *reinterpret_cast<f16x4*>(o + aorow * p.H + n) = v;
       }
     }
     if (!FUSED && nar > 0) {

@@ -4,6 +4,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Fused Stage 2 scatter-reduce (1): each weighted pair row is added straight
+// into its token's fp16 output row with packed fp16 atomics (the output is
+// zeroed first, and no combine runs), instead of (0, the default) a per-pair
+// row that the deterministic combine sums in choice order.  Off by default:
+// device-scope atomics on MI355X run far below plain stores.  A/B in one run
+// (2 x 2 interleaved): dsv3's step 5.26 -> 5.61 ms (Stage 2 1.855 -> 2.321 ms
+// against the combine's 0.090), mixtral 1.543 -> 1.583, w8a8 int8 0.890 ->
+// 1.178, fp8 0.833 -> 1.124, decode level (0.501 -> 0.499).  And the order of
+// the additions, so the fp16 rounding of the sum, varies from call to call.
+#ifndef MOE_S2_SCATTER
+#define MOE_S2_SCATTER 0
+#endif
+
 namespace moe {
 
 // Operand formats of the expert GEMMs: fp16, or 8-bit codes with fp32 row
@@ -71,7 +84,14 @@ struct Stage2Params {
   int host_blocks;          // BM-row blocks the row buffers hold (set by the launcher);
                             // pre-routed: blocks of the launch (gidx entries, clamped)
   int absorb = 0;           // fp16, 128-row paired items, E <= 256: absorbed rows; as in Stage 1
+  int topk = 0;             // fused, built with MOE_S2_SCATTER: choices per token; `out` is then
+                            // fp16 [T, H] (zeroed first) and each pair row is added to its token's
+                            // row with packed fp16 atomics
 };
+
+// Zeroes n bytes (n a multiple of 16, p 16-byte aligned) with vector stores:
+// a kernel, not hipMemsetAsync, so that it can be captured in a graph.
+hipError_t launch_zero(void* p, int64_t n, hipStream_t stream);
 
 // qt: a QuantType
 hipError_t launch_stage1(const Stage1Params& p, int block_m, int qt, bool gather,

@@ -471,6 +471,19 @@ hipError_t launch_combine(const void* y_pair, const int32_t* pos, int64_t T, int
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void zero_kernel(u32x4* __restrict__ p, int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n16) p[i] = u32x4{0, 0, 0, 0};
+}
+
+hipError_t launch_zero(void* p, int64_t n, hipStream_t s) {
+  const int64_t n16 = n / 16;
+  if (n16 == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<u32x4*>(p), n16);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Per-row symmetric int8: one wave per row, 8 fp16 per lane per chunk.  Rows
 // of up to 64 * 8 * NCH elements are held in registers (all NCH chunk loads

@@ -485,8 +485,10 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="also time the step captured once in a HIP graph (torch.cuda.graph) and replayed")
     ap.add_argument("--ep-shards", type=int, default=0,
-                    help="also time one expert-parallel shard (experts [0, E/G), moe_fused_forward_shard) at its "
-                         "real shape: the work one GPU of G does between dispatch and combine; fp16 only")
+                    help="also time one expert-parallel shard (experts [0, E/G)) at its real shape: from the "
+                         "logits over all tokens (moe_fused_forward_shard), and as one GPU of G runs it after the "
+                         "dispatch exchange, on the received tokens with their given routing "
+                         "(moe_fused_forward_routed); fp16 only")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the extra legs: run_kernel on the reference's cases 1-3 ('prerouted') and the "
                          "other BASELINE configs ('configs')")
@@ -732,17 +734,63 @@ def main():
         eargs = head + [P(inp[w_].data_ptr()) for w_ in ("wg", "wu", "wd")] + \
             [P(eout.data_ptr()), T, H, I, E, k, 0, n, sbm, P(ews.data_ptr()), ews.numel(), P(0), P(0), stream, P(0)]
         e_ms = timed(L.moe_fused_forward_shard, eargs, "moe_fused_forward_shard")
+        sev = HipEvents(7 * args.steps)
+        for i in range(args.steps):
+            check(L.moe_fused_forward_shard(*eargs[:-1], ctypes.cast(ctypes.byref(sev.ev, 7 * i * ctypes.sizeof(P)),
+                                                                       ctypes.POINTER(P))), "moe_fused_forward_shard")
+        torch.cuda.synchronize()
+        e_stage = {nm: round(statistics.mean(sev.elapsed_ms(7 * i + j, 7 * i + j + 1) for i in range(args.steps)), 4)
+                   for j, nm in enumerate(stage_names)}
+        sev.close()
         local = ids_np < n
         lp = int(local.sum())
         lt = int(np.unique(ids_np[local]).size)
         e_flops = 6.0 * H * I * lp
         e_bytes = lt * 3.0 * H * I * 2 + T * H * 2 * 2 + T * E * 4 + T * k * 8
         ep = {"shards": G, "experts_local": n, "pairs_local": lp, "experts_touched_local": lt,
-              "shard_ms": round(e_ms, 4), "tflops": round(e_flops / (e_ms * 1e-3) / 1e12, 2),
+              "shard_ms": round(e_ms, 4), "stage_ms": e_stage, "tflops": round(e_flops / (e_ms * 1e-3) / 1e12, 2),
               "gb_per_s": round(e_bytes / (e_ms * 1e-3) / 1e9, 1),
               "frac_of_roofline_time": round(max(e_flops / (PEAK_F16_TFLOPS * 1e12),
                                                  e_bytes / (PEAK_HBM_GBS * 1e9)) / (e_ms * 1e-3), 4),
               "shards_x_shard_ms_over_full_ms": round(G * e_ms / ms, 3)}
+        # The same shard as one GPU of an expert-parallel layout runs it after the dispatch
+        # exchange: only the tokens with a choice in the shard, gathered (outside the timed
+        # region) with their global ids and weights; no routing, and one partial row per
+        # received token out (moe_fused_forward_routed).
+        tok = torch.from_numpy(np.flatnonzero(local.any(axis=1))).to(dev)
+        R = int(tok.numel())
+        xr, ir, wr_ = inp["x"][tok].contiguous(), ids[tok].contiguous(), wts[tok].contiguous()
+        rout = torch.full((R, H), float("nan"), dtype=torch.float16, device=dev)
+        rws = torch.empty(int(L.moe_fused_routed_workspace_bytes(R, H, I, E, k, n, sbm)), dtype=torch.uint8, device=dev)
+        rargs = [P(xr.data_ptr()), P(ir.data_ptr()), P(wr_.data_ptr())] + \
+            [P(inp[w_].data_ptr()) for w_ in ("wg", "wu", "wd")] + \
+            [P(rout.data_ptr()), R, H, I, E, k, 0, n, sbm, P(rws.data_ptr()), rws.numel(), stream, P(0)]
+        d_ms = timed(L.moe_fused_forward_routed, rargs, "moe_fused_forward_routed")
+        dev_ = HipEvents(7 * args.steps)
+        for i in range(args.steps):
+            check(L.moe_fused_forward_routed(*rargs[:-1], ctypes.cast(ctypes.byref(dev_.ev, 7 * i * ctypes.sizeof(P)),
+                                                                        ctypes.POINTER(P))), "moe_fused_forward_routed")
+        torch.cuda.synchronize()
+        d_stage = {nm: round(statistics.mean(dev_.elapsed_ms(7 * i + j, 7 * i + j + 1) for i in range(args.steps)), 4)
+                   for j, nm in enumerate(stage_names) if nm not in ("route", "quant_x")}
+        dev_.close()
+        d_bytes = lt * 3.0 * H * I * 2 + R * H * 2 * 2 + R * k * 8
+        ep["dispatched"] = {
+            "tokens_received": R, "ms": round(d_ms, 4), "stage_ms": d_stage,
+            "tflops": round(e_flops / (d_ms * 1e-3) / 1e12, 2), "gb_per_s": round(d_bytes / (d_ms * 1e-3) / 1e9, 1),
+            "roofline_ideal_ms": round(max(e_flops / (PEAK_F16_TFLOPS * 1e12), d_bytes / (PEAK_HBM_GBS * 1e9)) * 1e3, 4),
+            "frac_of_roofline_time": round(max(e_flops / (PEAK_F16_TFLOPS * 1e12),
+                                               d_bytes / (PEAK_HBM_GBS * 1e9)) / (d_ms * 1e-3), 4)}
+        if not args.no_check:
+            from oracle import fused_moe_forward
+            pick = torch.from_numpy(np.sort(np.random.default_rng(5).choice(R, min(R, 32), replace=False))).to(dev)
+            ref = fused_moe_forward(xr[pick].cpu(), None, inp["wg"][:n], inp["wu"][:n], inp["wd"][:n], k,
+                                    expert_range=(0, n), routing=(ir[pick].cpu(), wr_[pick].cpu())).float()
+            got = rout[pick].float().cpu()
+            ep["dispatched"]["check"] = {
+                "tokens_checked": int(pick.numel()), "output_all_finite": bool(torch.isfinite(rout).all()),
+                "within_rtol2e-2_atol1e-2": bool(torch.isfinite(got).all()) and
+                bool(((got - ref).abs() <= 1e-2 + 2e-2 * ref.abs()).all())}
 
     copy_gbs = calib_copy(dev) if args.calib_copy else None
 

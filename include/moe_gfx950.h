@@ -22,7 +22,8 @@
  * Extensions with no reference counterpart (each documented below): the
  * router GEMM (moe_route_hidden, moe_fused_forward_hidden), the shared expert
  * (moe_fused_forward_shared), strided weights (moe_fused_forward_ex), one
- * expert-parallel shard (moe_fused_forward_shard) and the fp8 variant
+ * expert-parallel shard (moe_fused_forward_shard), a caller-given routing
+ * (moe_fused_forward_routed) and the fp8 variant
  * (moe_quantize_rows_fp8, moe_fused_forward_fp8).
  */
 #ifndef MOE_GFX950_H
@@ -262,6 +263,29 @@ int moe_fused_forward_shard(const void* x, const float* logits, const float* bia
                             int64_t E_total, int64_t k, int64_t expert_begin, int64_t E_local, int64_t block_m,
                             void* workspace, int64_t workspace_bytes, int32_t* topk_ids_out,
                             float* topk_weights_out, void* stream, void* const* stage_events);
+
+/* moe_fused_forward_routed: the same expert work from a routing given by the
+ * caller -- what one GPU runs after an expert-parallel dispatch, or any caller
+ * whose router this library does not implement.  x fp16 [T, H] holds the
+ * tokens (e.g. the rows a dispatch delivered), topk_ids int32 [T, k] their
+ * global expert ids and topk_weights fp32 [T, k] their weights, used as given
+ * (no renormalisation).  out fp16 [T, H]: out[t] = sum, in choice order, over
+ * the choices j with expert_begin <= topk_ids[t, j] < expert_begin + E_local
+ * of topk_weights[t, j] * FFN_{topk_ids[t, j] - expert_begin}(x[t]); any other
+ * id (another GPU's expert, or a negative "no choice" mark) adds nothing, and
+ * a token with no such choice gets 0.  The weights hold experts [expert_begin,
+ * expert_begin + E_local); E_total (the routing's expert count) only sets the
+ * block rows that block_m = 0 picks.  fp16, dense weights, no shared expert;
+ * workspace moe_fused_routed_workspace_bytes bytes; stage_events as for
+ * moe_fused_forward_events (its route marks are taken back to back), or NULL.
+ * No counterpart in the reference (problem_detail.json:18, :30: one device,
+ * routing outside the operator). */
+int64_t moe_fused_routed_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
+                                         int64_t E_local, int64_t block_m);
+int moe_fused_forward_routed(const void* x, const int32_t* topk_ids, const float* topk_weights, const void* w_gate,
+                             const void* w_up, const void* w_down, void* out, int64_t T, int64_t H, int64_t I,
+                             int64_t E_total, int64_t k, int64_t expert_begin, int64_t E_local, int64_t block_m,
+                             void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events);
 
 /* ------------------------------------------------------------------------
  * W8A8.  moe_quantize_rows_w8: per-row symmetric int8 of an fp16 [R, K]

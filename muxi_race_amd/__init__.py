@@ -10,6 +10,7 @@ from .moe import (  # noqa: F401
     MoeError,
     W8A8Weights,
     fused_moe,
+    fused_moe_routed,
     fused_workspace_bytes,
     moe_align,
     pick_block_m,

@@ -42,6 +42,9 @@ SIGNATURES = {
     "moe_fused_shard_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "moe_fused_forward_shard": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _p, _i64, _p, _p, _p, _p]),
+    "moe_fused_routed_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "moe_fused_forward_routed": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _i64, _p, _i64, _p, _p]),
     "moe_fused_shared_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "moe_fused_forward_shared": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                         _i64, _i64, _p, _i64, _p, _p, _p]),

@@ -277,6 +277,9 @@ int64_t moe_fused_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, in
 // The always-on shared expert (wg_s / wu_s / wd_s non-null, fp16 only) runs as
 // expert E: every token takes it as choice k with weight 1, so the pipeline
 // works on E + 1 experts and k + 1 choices and the combine adds it last.
+// ids_in / w_in (both non-null): the routing is given, int32 [T, k] ids and
+// fp32 [T, k] weights, instead of computed from logits or the router weight;
+// choices whose id lies outside [e_begin, e_begin + E) add nothing.
 static int fused_common(int qt, const void* x, const float* logits, const void* w_router, const float* bias,
                         const void* wg, const float* sg, const void* wu, const float* su,
                         const void* wd, const float* sd, const void* wg_s, const void* wu_s,
@@ -284,8 +287,9 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
                         void* out, int64_t T, int64_t H,
                         int64_t I, int64_t E, int64_t k, int64_t block_m, void* workspace,
                         int64_t workspace_bytes, int32_t* ids_out, float* w_out, void* stream,
-                        void* const* ev) {
+                        void* const* ev, const int32_t* ids_in = nullptr, const float* w_in = nullptr) {
   const bool w8 = qt != moe::kQF16;  // 8-bit operands: int8 or fp8
+  const bool given = ids_in || w_in;  // routing given by the caller
   // expert shard: routing over E_route experts, this call's weights hold
   // experts [e_begin, e_begin + E); only their pairs are computed and summed
   const bool shard = E_route > 0;
@@ -293,6 +297,8 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   if (shard && (e_begin < 0 || E <= 0 || e_begin + E > E_route || w_router || wg_s || wu_s || wd_s))
     return fail(MOE_ERR_INVALID_ARG, "expert shard [%lld, %lld) of %lld experts (logits only, no shared expert)",
                 (long long)e_begin, (long long)(e_begin + E), (long long)E_route);
+  if (given && (!shard || logits || !ids_in || !w_in))
+    return fail(MOE_ERR_INVALID_ARG, "a given routing takes ids and weights, no logits, and an expert range");
   const bool shared = wg_s || wu_s || wd_s;
   if (shared && (w8 || !wg_s || !wu_s || !wd_s))
     return fail(w8 ? MOE_ERR_UNSUPPORTED : MOE_ERR_INVALID_ARG, w8 ? "the shared expert is supported on the fp16 path" : "null pointer argument");
@@ -303,7 +309,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   int rc = check_dims(T, H, I, shard ? E_route : Ee, ke, block_m);
   if (rc) return rc;
   if (T == 0) return MOE_OK;
-  if (!x || (!logits && !w_router) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
+  if (!x || (!logits && !w_router && !given) || !wg || !wu || !wd || !out || !workspace || (w8 && (!sg || !su || !sd)))
     return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
   if (w_router && (rc = check_router(x, w_router, T, H, E, k))) return rc;
   // weight strides in elements, {row, expert} of gate/up then of down (null
@@ -333,8 +339,11 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   const int64_t bm2 = block_m == 256 && qt == moe::kQF16 && MOE_S2_F16_256 == 0 ? 128 : block_m;
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
+  // routing written by route / router (ids, wts), read by align, Stage 2 and the combine (rids, rwts)
   int32_t* ids = ids_out ? ids_out : (int32_t*)(ws + L.ids);
   float* wts = w_out ? w_out : (float*)(ws + L.w);
+  const int32_t* rids = given ? ids_in : ids;
+  const float* rwts = given ? w_in : wts;
   int32_t* sorted = (int32_t*)(ws + L.sorted);
   int32_t* gs = (int32_t*)(ws + L.gs);
   int32_t* go = (int32_t*)(ws + L.go);
@@ -346,13 +355,15 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   // [4] stage 1, [5] stage 2, [6] combined
   auto mark = [&](int i) { if (ev && ev[i]) (void)hipEventRecord((hipEvent_t)ev[i], s); };
   mark(0);
-  if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
+  if (given) {
+    // routed by the caller: nothing to launch (ids and weights are only read)
+  } else if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
     if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s, e_shared), "router"))) return rc;
   } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E_route, (int)k, ids, wts, s, e_shared), "route_topk"))) {
     return rc;
   }
   mark(1);
-  if ((rc = check_launch(moe::launch_align(ids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s, (int)e_begin), "align"))) return rc;
+  if ((rc = check_launch(moe::launch_align(rids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s, (int)e_begin), "align"))) return rc;
   mark(2);
   if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, ws + L.xq, (float*)(ws + L.sx), qt, s), "quantize_x"))) return rc;
   mark(3);
@@ -399,7 +410,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   p2.topk = (int)ke;
   p2.pos = (int32_t*)(ws + L.pos);
   p2.absorb = 1;  // as in Stage 1
-  p2.routed = wts;
+  p2.routed = rwts;
   p2.routed_f16 = 0;
   p2.gs = gs;
   p2.go = go;
@@ -420,7 +431,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
     return MOE_OK;
   }
   rc = check_launch(moe::launch_combine(ws + L.ypair, (const int32_t*)(ws + L.pos), T, H, (int)ke, out, s,
-                                        shard ? ids : nullptr, (int)e_begin, (int)E),
+                                        shard ? rids : nullptr, (int)e_begin, (int)E),
                     "combine");
   mark(6);
   return rc;
@@ -511,6 +522,22 @@ int moe_fused_forward_shard(const void* x, const float* logits, const float* bia
   return fused_common(moe::kQF16, x, logits, nullptr, bias, w_gate, nullptr, w_up, nullptr, w_down, nullptr, nullptr,
                       nullptr, nullptr, nullptr, expert_begin, E_total, out, T, H, I, E_local, k, block_m, workspace,
                       workspace_bytes, topk_ids_out, topk_weights_out, stream, stage_events);
+}
+
+int64_t moe_fused_routed_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E_total, int64_t k,
+                                         int64_t E_local, int64_t block_m) {
+  return moe_fused_shard_workspace_bytes(T, H, I, E_total, k, E_local, block_m);
+}
+
+int moe_fused_forward_routed(const void* x, const int32_t* topk_ids, const float* topk_weights, const void* w_gate,
+                             const void* w_up, const void* w_down, void* out, int64_t T, int64_t H, int64_t I,
+                             int64_t E_total, int64_t k, int64_t expert_begin, int64_t E_local, int64_t block_m,
+                             void* workspace, int64_t workspace_bytes, void* stream, void* const* stage_events) {
+  if (E_total <= 0) return fail(MOE_ERR_INVALID_ARG, "E_total=%lld", (long long)E_total);
+  if (T > 0 && (!topk_ids || !topk_weights)) return fail(MOE_ERR_INVALID_ARG, "null pointer argument");
+  return fused_common(moe::kQF16, x, nullptr, nullptr, nullptr, w_gate, nullptr, w_up, nullptr, w_down, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, expert_begin, E_total, out, T, H, I, E_local, k, block_m,
+                      workspace, workspace_bytes, nullptr, nullptr, stream, stage_events, topk_ids, topk_weights);
 }
 
 }  // extern "C"

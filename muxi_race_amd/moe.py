@@ -282,6 +282,53 @@ def quantize_w8a8_weights(w_gate, w_up, w_down, fmt: str = "int8") -> W8A8Weight
 # ---------------------------------------------------------------------------
 # north-star entry point
 # ---------------------------------------------------------------------------
+def fused_moe_routed(hidden_states, topk_ids, topk_weights, w_gate, w_up, w_down, *, expert_begin: int = 0,
+                     num_experts: int | None = None, block_m: int = 0, out=None, stage_events=None):
+    """The fused expert MLPs and weighted combine from a routing computed
+    elsewhere: what one GPU runs after an expert-parallel dispatch (the
+    received token rows, their global top-k ids and weights), or any caller
+    whose router this library does not implement.  hidden_states fp16 [T, H],
+    topk_ids int32 [T, k], topk_weights fp32 [T, k] (used as given, not
+    renormalised), w_gate/w_up fp16 [E, I, H] and w_down fp16 [E, H, I] for
+    experts [expert_begin, expert_begin + E).  Returns fp16 [T, H]: each token's
+    sum, in choice order, of weight * expert MLP over its choices in that
+    range; other ids (another GPU's experts, or -1 for "no choice") add
+    nothing.  ``num_experts`` (the routing's expert count, default
+    expert_begin + E) only sets the block rows the library picks."""
+    x = hidden_states
+    _need(x, "hidden_states", (torch.float16,), 2)
+    dev = x.device
+    T, H = x.shape
+    _need(topk_ids, "topk_ids", (torch.int32,), 2, dev)
+    _need(topk_weights, "topk_weights", (torch.float32,), 2, dev)
+    if topk_ids.shape[0] != T or tuple(topk_weights.shape) != tuple(topk_ids.shape):
+        raise ValueError("topk_ids and topk_weights must both be [T, k]")
+    k = topk_ids.shape[1]
+    for name, t in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down)):
+        _need(t, name, (torch.float16,), 3, dev)
+    E, I = w_gate.shape[0], w_gate.shape[1]
+    if tuple(w_gate.shape) != (E, I, H) or tuple(w_up.shape) != (E, I, H) or tuple(w_down.shape) != (E, H, I):
+        raise ValueError("expert weight shapes do not match [E,I,H]/[E,I,H]/[E,H,I]")
+    E_total = expert_begin + E if num_experts is None else int(num_experts)
+    if expert_begin < 0 or expert_begin + E > E_total:
+        raise ValueError(f"experts [{expert_begin}, {expert_begin + E}) outside the {E_total} routed experts")
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    else:
+        _need(out, "out", (torch.float16,), 2, dev)
+        if tuple(out.shape) != (T, H):
+            raise ValueError("out shape mismatch")
+    L = lib()
+    ws = _workspace(dev, ("fused", None),
+                    L.moe_fused_routed_workspace_bytes(T, H, I, E_total, k, E, block_m))
+    with torch.cuda.device(dev):
+        rc = L.moe_fused_forward_routed(_ptr(x), _ptr(topk_ids), _ptr(topk_weights), _ptr(w_gate), _ptr(w_up),
+                                        _ptr(w_down), _ptr(out), T, H, I, E_total, k, expert_begin, E, block_m,
+                                        _ptr(ws), ws.numel(), _stream(dev), stage_events)
+    check(rc, "fused_moe_routed")
+    return out
+
+
 def fused_moe(hidden_states, router_logits, w_gate, w_up, w_down, top_k: int, *,
               expert_bias=None, w8a8: W8A8Weights | None = None, block_m: int = 0, out=None,
               return_routing: bool = False, router_weight=None, shared_expert=None, expert_range=None):

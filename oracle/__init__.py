@@ -41,6 +41,14 @@ Pinning (how each function is checked independently of its own formula):
                            gate (tests/test_oracle_fp8.py).
 * ``fused_moe_forward(shared=)`` -- exact doubling closed form and the dense
                            SwiGLU difference (tests/test_oracle_core.py).
+* ``fused_moe_forward(expert_range=)`` -- one shard over all experts is the
+                           full layer exactly, disjoint shards sum to it, dense
+                           fp64 per-token sums (tests/test_oracle_core.py).
+* ``fused_moe_forward(routing=)`` -- the router's own ids / weights reproduce
+                           the logits path bitwise (layer and shard), -1 or
+                           foreign ids equal zero weights exactly, dense fp64
+                           per-token sums with unnormalised weights
+                           (tests/test_oracle_core.py).
 * ``stratified_tokens`` -- (a sampler, not arithmetic) every block of the
                            routing's align holds a sampled token's pair, every
                            expert's first and last pair is sampled

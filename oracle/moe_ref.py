@@ -234,7 +234,8 @@ def combine(y_pair: torch.Tensor, T: int, top_k: int) -> torch.Tensor:
 
 
 def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
-                      block_m: int = 128, *, return_aux=False, experts=None, shared=None, expert_range=None):
+                      block_m: int = 128, *, return_aux=False, experts=None, shared=None, expert_range=None,
+                      routing=None):
     """Full MoE: route -> align -> gather -> pre-routed MLP -> weighted combine.
 
     Returns float16 [T, H] (and the routing/alignment intermediates when
@@ -247,13 +248,26 @@ def fused_moe_forward(x, logits, w_gate, w_up, w_down, top_k: int, bias=None,
     expert shard -- routing over all logits columns, weights of experts
     [begin, begin + count) only, and the sum over each token's choices routed
     there (other choices go to an appended all-zero expert with weight 0, which
-    adds exactly 0).
+    adds exactly 0).  ``routing`` = (ids int [T, k], weights float32 [T, k])
+    replaces the router (logits and bias are then ignored): the weights are
+    used as given, and with ``expert_range`` any id outside the range (another
+    shard's expert, or a negative "no choice" mark) adds nothing, as for the
+    other shards' choices above (build-defined: the step after an
+    expert-parallel dispatch; the reference has no routing, problem_detail.json:18).
     """
     x = _as_t(x)
     T, H = x.shape
     E = int(w_gate.shape[0])
-    ids, w = route_topk(_as_t(logits).float().numpy(), top_k,
-                        None if bias is None else _as_t(bias).float().numpy())
+    if routing is not None:
+        ids = np.asarray(_as_t(routing[0]).numpy(), dtype=np.int64).astype(np.int32)
+        w = np.asarray(_as_t(routing[1]).float().numpy(), dtype=np.float32)
+        if ids.shape != (T, top_k) or w.shape != (T, top_k):
+            raise ValueError("routing must be ([T, k] ids, [T, k] weights)")
+        if expert_range is None and ((ids < 0) | (ids >= E)).any():
+            raise ValueError("routing ids outside [0, E) need an expert_range")
+    else:
+        ids, w = route_topk(_as_t(logits).float().numpy(), top_k,
+                            None if bias is None else _as_t(bias).float().numpy())
     ids_global = ids
     if expert_range is not None:
         b, n = expert_range

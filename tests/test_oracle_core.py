@@ -245,3 +245,49 @@ def test_expert_shards_closed_forms(rng):
                 g, u = wg[e].double() @ x[t].double(), wu[e].double() @ x[t].double()
                 exp[t] += float(w[t, j]) * (wd[e].double() @ (torch.sigmoid(g) * g * u))
     torch.testing.assert_close(parts[2].double(), exp, rtol=2e-3, atol=2e-3)
+
+
+def test_given_routing_closed_forms(rng):
+    """A routing given instead of logits (the step after an expert-parallel
+    dispatch): (1) the router's own ids and weights reproduce the logits path
+    bitwise, whole layer and shard; (2) ids marked -1 or naming another
+    shard's experts add nothing, exactly as a weight of 0 would; (3) arbitrary,
+    unnormalised weights give the dense fp64 per-token sum w * MLP over the
+    in-range choices (a renormalisation or a dropped weight fails it)."""
+    T, H, I, E, k = 29, 32, 16, 8, 3
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16))
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    wg = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wu = torch.from_numpy((rng.standard_normal((E, I, H)) * 0.2).astype(np.float16))
+    wd = torch.from_numpy((rng.standard_normal((E, H, I)) * 0.2).astype(np.float16))
+    ids, w = route_topk(logits.numpy(), k)
+    full = fused_moe_forward(x, logits, wg, wu, wd, k)
+    assert torch.equal(fused_moe_forward(x, None, wg, wu, wd, k, routing=(ids, w)), full)
+    b, n = 2, 4
+    shard = fused_moe_forward(x, logits, wg[b:b + n], wu[b:b + n], wd[b:b + n], k, expert_range=(b, n))
+    given = fused_moe_forward(x, None, wg[b:b + n], wu[b:b + n], wd[b:b + n], k, expert_range=(b, n),
+                              routing=(ids, w))
+    assert torch.equal(given, shard)
+    # out-of-range marks == zero weights
+    ids2 = ids.copy()
+    drop = rng.random(ids.shape) < 0.3
+    ids2[drop] = -1
+    w0 = np.where(drop, np.float32(0), w).astype(np.float32)
+    a = fused_moe_forward(x, None, wg, wu, wd, k, expert_range=(0, E), routing=(ids2, w))
+    z = fused_moe_forward(x, None, wg, wu, wd, k, routing=(ids, w0))
+    assert torch.equal(a, z)
+    # unnormalised weights, ids across a wider routing (E_total = 12)
+    ids3 = rng.integers(-1, 12, size=(T, k)).astype(np.int32)
+    w3 = (rng.random((T, k)) * 3).astype(np.float32)
+    got = fused_moe_forward(x, None, wg[b:b + n], wu[b:b + n], wd[b:b + n], k, expert_range=(b, n),
+                            routing=(ids3, w3))
+    exp = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        for j in range(k):
+            e = int(ids3[t, j])
+            if b <= e < b + n:
+                g, u = wg[e].double() @ x[t].double(), wu[e].double() @ x[t].double()
+                exp[t] += float(w3[t, j]) * (wd[e].double() @ (torch.sigmoid(g) * g * u))
+    torch.testing.assert_close(got.double(), exp, rtol=2e-3, atol=2e-3)
+    with pytest.raises(ValueError):
+        fused_moe_forward(x, None, wg, wu, wd, k, routing=(ids3, w3))  # out-of-range ids need a range

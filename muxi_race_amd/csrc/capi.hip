@@ -355,8 +355,15 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   // [4] stage 1, [5] stage 2, [6] combined
   auto mark = [&](int i) { if (ev && ev[i]) (void)hipEventRecord((hipEvent_t)ev[i], s); };
   mark(0);
+  // 8-bit operands from logits: the routing and the per-token quantisation of
+  // x run as one launch (route_quant_kernel)
+  const bool route_quant = w8 && !given && !w_router;
   if (given) {
     // routed by the caller: nothing to launch (ids and weights are only read)
+  } else if (route_quant) {
+    if ((rc = check_launch(moe::launch_route_quant(logits, bias, (int)T, (int)E_route, (int)k, ids, wts, x, H,
+                                                   ws + L.xq, (float*)(ws + L.sx), qt, s), "route_quantize_x")))
+      return rc;
   } else if (w_router) {  // router GEMM + routing; its partial sums sit after the fused workspace
     if ((rc = check_launch(moe::launch_router(x, w_router, bias, (int)T, H, (int)E, (int)k, ids, wts, nullptr, (float*)(ws + L.total), s, e_shared), "router"))) return rc;
   } else if ((rc = check_launch(moe::launch_route_topk(logits, bias, (int)T, (int)E_route, (int)k, ids, wts, s, e_shared), "route_topk"))) {
@@ -365,7 +372,7 @@ static int fused_common(int qt, const void* x, const float* logits, const void* 
   mark(1);
   if ((rc = check_launch(moe::launch_align(rids, (int)(T * ke), (int)Ee, (int)block_m, sorted, (int32_t*)(ws + L.bexp), gs, go, gpo, (int32_t*)(ws + L.whist), s, (int)e_begin), "align"))) return rc;
   mark(2);
-  if (w8 && (rc = check_launch(moe::launch_quant_rows(x, T, H, ws + L.xq, (float*)(ws + L.sx), qt, s), "quantize_x"))) return rc;
+  if (w8 && !route_quant && (rc = check_launch(moe::launch_quant_rows(x, T, H, ws + L.xq, (float*)(ws + L.sx), qt, s), "quantize_x"))) return rc;
   mark(3);
 
   moe::Stage1Params p1{};

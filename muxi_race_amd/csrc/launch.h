@@ -134,6 +134,11 @@ hipError_t launch_router(const void* x, const void* w_router, const float* bias,
 // y_pair row of pair t*k + j: pos[t*k + j].
 hipError_t launch_combine(const void* y_pair, const int32_t* pos, int64_t T, int64_t H, int k, void* out,
                           hipStream_t stream, const int32_t* ids = nullptr, int e_lo = 0, int e_n = 0);
+// Routing (as launch_route_topk, no shared expert) and the per-token 8-bit
+// quantisation of x [T, H] (as launch_quant_rows) in one launch.
+hipError_t launch_route_quant(const float* logits, const float* bias, int T, int E, int k, int32_t* ids,
+                              float* w, const void* x, int64_t H, void* xq, float* sx, int qt,
+                              hipStream_t stream);
 // Per-row 8-bit quantisation of an fp16 [R, K] matrix to the format qt
 // (kQI8 or kQF8): codes into q, amax / qmax into scale.  With `ids` set only
 // rows r < *used_rows (a device value) with ids[r] < sentinel are quantised

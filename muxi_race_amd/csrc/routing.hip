@@ -495,6 +495,69 @@ __device__ __forceinline__ u32x2 quant_pack8(f16x8 v, float inv) {
                quant_code4<F8>((float)v[4], (float)v[5], (float)v[6], (float)v[7], inv)};
 }
 
+// One wave quantises one row of K fp16 values: amax over the row, codes of
+// x * (qmax / amax) into qrow, amax / qmax into *scale (written by lane 0).
+// Rows of up to 512 * NCH values are held in registers: quant_row_load issues
+// every load of the row at once, quant_row_store finishes the row, so a
+// caller can run other work while the loads are in flight.
+// Every load is unconditional (a chunk past the row reads the row's last
+// chunk and is zeroed by a select): a predicated load compiles to a branch
+// that waits for all earlier loads, which serialised the row's loads.
+// K is a positive multiple of 8.
+template <int NCH>
+__device__ __forceinline__ void quant_row_load(const _Float16* __restrict__ row, int64_t K, f16x8 (&v)[NCH]) {
+  const int l = lane_id();
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t c = 512 * j + 8 * l;
+    v[j] = *reinterpret_cast<const f16x8*>(row + (c < K ? c : K - 8));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before any use of a result
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    if (512 * j + 8 * l >= K) v[j] = f16x8{};
+}
+template <int NCH, bool F8>
+__device__ __forceinline__ void quant_row_store(const f16x8 (&v)[NCH], int64_t K, uint8_t* __restrict__ qrow,
+                                                float* __restrict__ scale) {
+  const int l = lane_id();
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[j][i]));
+  amax = wave_max(amax);
+  const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t c = 512 * j + 8 * l;
+    if (c < K) *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(v[j], inv);
+  }
+  if (l == 0) *scale = amax / qmax<F8>();
+}
+template <int NCH, bool F8>
+__device__ __forceinline__ void quant_row_wave(const _Float16* __restrict__ row, int64_t K,
+                                               uint8_t* __restrict__ qrow, float* __restrict__ scale) {
+  if constexpr (NCH > 0) {
+    f16x8 v[NCH];
+    quant_row_load<NCH>(row, K, v);
+    quant_row_store<NCH, F8>(v, K, qrow, scale);
+  } else {
+    const int l = lane_id();
+    float amax = 0.0f;
+    for (int64_t c = 8 * l; c < K; c += 512) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
+    }
+    amax = wave_max(amax);
+    const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
+    for (int64_t c = 8 * l; c < K; c += 512)
+      *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(*reinterpret_cast<const f16x8*>(row + c), inv);
+    if (l == 0) *scale = amax / qmax<F8>();
+  }
+}
+
 //
 // With `ids` set, row r is quantised only if r < *used_rows and ids[r] <
 // sentinel: the intermediate's rows in the expert-sorted space, where rows
@@ -507,42 +570,86 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
                                                          const int32_t* __restrict__ ids, int32_t sentinel,
                                                          const int32_t* __restrict__ used_rows) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int l = lane_id();
   if (r >= R) return;
   if (ids && (r >= *used_rows || ids[r] >= sentinel)) return;
-  const _Float16* row = w + r * K;
-  uint8_t* qrow = q + r * K;
-  float amax = 0.0f;
+  quant_row_wave<NCH, F8>(w + r * K, K, q + r * K, scale + r);
+}
+
+// Routing of token t (as route_topk_kernel) and, in the same wave, the 8-bit
+// quantisation of its activation row x[t] (as quant_rows_kernel): both are
+// per-token passes over independent inputs, so the 8-bit paths run them as
+// one launch instead of two, with the row's loads issued before the routing
+// so that their latency overlaps it.
+template <int VPL, int NCH, bool F8>
+__global__ __launch_bounds__(256) void route_quant_kernel(const float* __restrict__ logits,
+                                                          const float* __restrict__ bias, int T, int E, int k,
+                                                          int32_t* __restrict__ ids, float* __restrict__ wout,
+                                                          const _Float16* __restrict__ x, int64_t H,
+                                                          uint8_t* __restrict__ xq, float* __restrict__ sx) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // uniform per wave
+  const float* row = logits + (int64_t)t * E;
   if constexpr (NCH > 0) {
+    // logits (and bias) first, then the row: loads retire in order, so the
+    // routing waits only for its own values while the row is in flight
+    const int l = lane_id();
+    float lv[VPL], bv[VPL];
+    uint32_t valid = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = l + 64 * j;
+      lv[j] = -INFINITY;
+      bv[j] = 0.0f;
+      if (e < E) {
+        lv[j] = row[e];
+        if (bias) bv[j] = bias[e];
+        valid |= 1u << j;
+      }
+    }
     f16x8 v[NCH];
+    quant_row_load<NCH>(x + (int64_t)t * H, H, v);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int64_t c = 512 * j + 8 * l;
-      v[j] = c < K ? *reinterpret_cast<const f16x8*>(row + c) : f16x8{};
-    }
-#pragma unroll
-    for (int j = 0; j < NCH; ++j)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[j][i]));
-    amax = wave_max(amax);
-    const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int64_t c = 512 * j + 8 * l;
-      if (c < K) *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(v[j], inv);
-    }
+    for (int j = 0; j < VPL; ++j)
+      if (bias && (valid & (1u << j))) lv[j] = lv[j] + bv[j];
+    route_token_values<VPL>(lv, valid, t, k, ids, wout, k, -1);
+    quant_row_store<NCH, F8>(v, H, xq + (int64_t)t * H, sx + t);
   } else {
-    for (int64_t c = 8 * l; c < K; c += 512) {
-      const f16x8 v = *reinterpret_cast<const f16x8*>(row + c);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
-    }
-    amax = wave_max(amax);
-    const float inv = amax > 0.0f ? qmax<F8>() / amax : 0.0f;
-    for (int64_t c = 8 * l; c < K; c += 512)
-      *reinterpret_cast<u32x2*>(qrow + c) = quant_pack8<F8>(*reinterpret_cast<const f16x8*>(row + c), inv);
+    route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout, k, -1);
+    quant_row_wave<NCH, F8>(x + (int64_t)t * H, H, xq + (int64_t)t * H, sx + t);
   }
-  if (l == 0) scale[r] = amax / qmax<F8>();
+}
+
+hipError_t launch_route_quant(const float* logits, const float* bias, int T, int E, int k, int32_t* ids,
+                              float* w, const void* x, int64_t H, void* xq, float* sx, int qt, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((T + 3) / 4), block(256);
+  const int vpl = (E + 63) / 64;
+  const int64_t nch = (H + 511) / 512;
+  const _Float16* xs = reinterpret_cast<const _Float16*>(x);
+  uint8_t* q = reinterpret_cast<uint8_t*>(xq);
+#define MOE_RQ2(V, N, F) \
+  hipLaunchKernelGGL((route_quant_kernel<V, N, F>), grid, block, 0, s, logits, bias, T, E, k, ids, w, xs, H, q, sx)
+#define MOE_RQ1(V, F)            \
+  do {                           \
+    if (nch <= 4) MOE_RQ2(V, 4, F);       \
+    else if (nch <= 8) MOE_RQ2(V, 8, F);  \
+    else if (nch <= 16) MOE_RQ2(V, 16, F); \
+    else MOE_RQ2(V, 0, F);                \
+  } while (0)
+#define MOE_RQ(V)                          \
+  do {                                     \
+    if (qt == kQF8) MOE_RQ1(V, true);      \
+    else MOE_RQ1(V, false);                \
+  } while (0)
+  if (vpl <= 1) MOE_RQ(1);
+  else if (vpl <= 2) MOE_RQ(2);
+  else if (vpl <= 4) MOE_RQ(4);
+  else if (vpl <= 8) MOE_RQ(8);
+  else MOE_RQ(16);
+#undef MOE_RQ
+#undef MOE_RQ1
+#undef MOE_RQ2
+  return hipGetLastError();
 }
 
 hipError_t launch_quant_rows(const void* w, int64_t R, int64_t K, void* q, float* scale, int qt,

@@ -120,8 +120,10 @@ __device__ __forceinline__ void barrier_no_fence() {
 // decode ring streamed 6.15 -> 7.12 TB/s at rows 14 KiB apart, 5.45 -> 6.14
 // TB/s at 4 KiB).  Weight tiles that sibling items of a multi-block
 // expert re-read from L2, and token / intermediate rows, keep the default
-// policy (non-temporal there measured slower: fewer L2 hits); the wide-tile
-// kernels load everything with the default policy (no gain measured there,
+// policy (non-temporal there measured slower: fewer L2 hits).  Of the
+// wide-tile kernels, only the 8-bit 256-row items stream their unshared
+// weight tiles (MOE_W8_STREAM in grouped_gemm.hip, measured faster there);
+// the fp16 ones load everything with the default policy (no gain measured,
 // and the per-instruction choice cost 2-5%).  0 turns streaming off.
 #ifndef MOE_W_POLICY
 #define MOE_W_POLICY 2

@@ -5,11 +5,12 @@ gate (relative L2 <= 5e-2) against the fp16 oracle.
 Elementwise against the fp16 oracle the W8A8 path is reported, not gated at
 100%: per-row weight int8 and per-token int8 of both activations (x and the
 SiLU*up intermediate) at H = 7168, I = 2048 leave ~3% relative L2, and about
-a quarter of the elements fall outside |d| <= 1e-2 + 5e-2 |ref| (a property of
+a fifth of the elements fall outside |d| <= 1e-2 + 5e-2 |ref| (a property of
 the quantisation scheme, the same for the oracle's own W8A8 arithmetic: 0.76
 inside on a T = 128, E = 8 slice of these dimensions).  The fraction inside
-is printed and held above 0.70.  Full-size outputs are NaN-poisoned and must
-come back finite; the w8a8 config's whole output is compared."""
+is printed and held above 0.80: the lowest case, the w8a8 config's whole
+output (2048 tokens), measures 0.818.  Full-size outputs are NaN-poisoned and
+must come back finite; the w8a8 config's whole output is compared."""
 import numpy as np
 import pytest
 import torch
@@ -20,7 +21,7 @@ from oracle import fused_moe_forward, quantize_rows_int8, route_topk, w8a8_forwa
 
 pytestmark = pytest.mark.gpu
 W8A8_REL_L2 = 5e-2
-W8A8_ELEMENTWISE_FLOOR = 0.70  # fraction within 1e-2 + 5e-2 |ref| of the fp16 oracle
+W8A8_ELEMENTWISE_FLOOR = 0.80  # fraction within 1e-2 + 5e-2 |ref| of the fp16 oracle (measured >= 0.818)
 
 
 @pytest.mark.parametrize("K", [1024, 2048 + 8, 7168, 8200])  # register path (4, 8, 16 chunks) and two-pass

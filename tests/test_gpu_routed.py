@@ -100,3 +100,35 @@ def test_routed_argument_errors():
         fused_moe_routed(inp["x"], ids, w, wg, wu, wd, expert_begin=2, num_experts=inp["E"])  # past E
     with pytest.raises((ValueError, MoeError)):
         fused_moe_routed(inp["x"], ids, w, wg[:, :, :-1], wu, wd)         # bad weight shape
+
+
+def test_routed_edge_cases():
+    """An empty batch returns at once; a token that lists the same expert twice
+    gets both pairs (two rows summed, as the oracle's align keeps both); k = 1
+    with weights of 1 is the plain per-expert MLP."""
+    from muxi_race_amd import fused_moe_routed
+    inp = moe_inputs("small", 105, T=96)
+    T, H, E = inp["T"], inp["H"], inp["E"]
+    wg, wu, wd = inp["wg"], inp["wu"], inp["wd"]
+    empty = fused_moe_routed(inp["x"][:0], torch.zeros((0, 2), dtype=torch.int32, device="cuda"),
+                             torch.zeros((0, 2), device="cuda"), wg, wu, wd)
+    assert empty.shape == (0, H)
+    g = torch.Generator().manual_seed(11)
+    ids = torch.randint(0, E, (T, 3), generator=g, dtype=torch.int32)
+    ids[:, 1] = ids[:, 0]  # every token lists its first expert twice
+    w = torch.rand((T, 3), generator=g)
+    got = fused_moe_routed(inp["x"], ids.cuda(), w.cuda(), wg, wu, wd)
+    ref = fused_moe_forward(inp["x"].cpu(), None, wg, wu, wd, 3, expert_range=(0, E), routing=(ids, w))
+    assert_close(got, ref, what="duplicate choices")
+    one = torch.randint(0, E, (T, 1), generator=g, dtype=torch.int32)
+    got1 = fused_moe_routed(inp["x"], one.cuda(), torch.ones((T, 1), device="cuda"), wg, wu, wd)
+    torch.cuda.synchronize()
+    xd = inp["x"].cpu().double()
+    exp = torch.zeros(T, H, dtype=torch.float64)
+    for e in range(E):
+        rows = (one[:, 0] == e).nonzero().flatten()
+        if rows.numel():
+            g_ = xd[rows] @ wg[e].cpu().double().T
+            u_ = xd[rows] @ wu[e].cpu().double().T
+            exp[rows] = (torch.sigmoid(g_) * g_ * u_) @ wd[e].cpu().double().T
+    assert_close(got1, exp, what="k = 1, weight 1: the per-expert MLP")

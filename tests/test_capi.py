@@ -82,6 +82,30 @@ def test_host_validation_without_gpu():
         assert rc == -1 and b"weight strides" in L.moe_last_error_string(), st
 
 
+def test_routed_entry_host_validation_without_gpu():
+    """moe_fused_forward_routed rejects a missing routing, an expert range past
+    the routing's experts and a bad block_m on the host; an empty batch is a
+    no-op; its workspace is the shard's (same layout)."""
+    from muxi_race_amd._lib import lib
+    L = lib()
+    nul, one = ctypes.c_void_p(0), ctypes.c_void_p(256)
+    args = lambda ids, w, T, E_total, b, E_local, bm: (one, ids, w, one, one, one, one, T, 128, 128, E_total, 2, b,
+                                                       E_local, bm, one, 1 << 30, nul, nul)
+    rc = L.moe_fused_forward_routed(*args(nul, nul, 4, 8, 0, 8, 0))
+    assert rc == -1 and b"null" in L.moe_last_error_string()
+    rc = L.moe_fused_forward_routed(*args(one, nul, 4, 8, 0, 8, 0))
+    assert rc == -1
+    rc = L.moe_fused_forward_routed(*args(one, one, 4, 8, 4, 8, 0))   # experts [4, 12) of 8
+    assert rc == -1 and b"expert shard" in L.moe_last_error_string()
+    rc = L.moe_fused_forward_routed(*args(one, one, 4, 8, 0, 8, 48))
+    assert rc == -2 and b"block_m" in L.moe_last_error_string()
+    rc = L.moe_fused_forward_routed(*args(one, one, 4, 0, 0, 8, 0))
+    assert rc == -1 and b"E_total" in L.moe_last_error_string()
+    assert L.moe_fused_forward_routed(*args(nul, nul, 0, 8, 0, 8, 0)) == 0  # T = 0
+    assert L.moe_fused_routed_workspace_bytes(2736, 7168, 2048, 256, 8, 32, 0) == \
+        L.moe_fused_shard_workspace_bytes(2736, 7168, 2048, 256, 8, 32, 0)
+
+
 def test_capacity_and_workspace_sizes():
     from muxi_race_amd._lib import lib
     L = lib()

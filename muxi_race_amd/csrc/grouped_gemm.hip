@@ -56,6 +56,17 @@
 #ifndef MOE_W8_STREAM
 #define MOE_W8_STREAM 1
 #endif
+// Triple items (moe_common.h schedule_absorbed) for fp16 Stage 1 on paired
+// 128-row items: an expert with an odd number (>= 3) of blocks streams each
+// half weight tile once, for its last three blocks together, instead of once
+// for a pair and again for a single block (1); 0, the default: pairs and a
+// single.  Off because it measured slower: A/B at dsv3 in one run, 3 x 3
+// interleaved, Stage 1 3.294 ms (pairs and singles) against 3.364-3.371
+// (triples, loads issued in one burst after the barrier) and 3.415-3.428 (the
+// token slot's loads spread over the first three sub-steps instead).
+#ifndef MOE_S1_TRIPLE
+#define MOE_S1_TRIPLE 0
+#endif
 // Stage 2 output through LDS as whole row segments (1) or direct 16-byte
 // pieces of 32 rows per store (0).
 #ifndef MOE_S2_STAGED_OUT
@@ -113,6 +124,115 @@ __device__ __forceinline__ void with_live(int live, F&& f) {
   }
 }
 
+// Stage 1 triple item (fp16, kBN-row blocks, 8 waves): 3 * kBN = 384 token
+// rows x (64 gate + 64 up) weight rows of one half tile.  Waves are 4 (M) x 2
+// (N), each owning 96 token rows x 32 features: three 32x32 blocks of gate
+// and three of up.  A whole stage would be 64 KiB, and two of them would
+// leave one in flight, so the ring is split as the 8-bit 256-row one: two
+// 48 KiB token slots and three 16 KiB weight slots (144 KiB).  After step j's
+// barrier T(j+1) and then W(j+2) are issued: the weight rows (HBM misses) run
+// two steps ahead, the token rows (L2 hits) one, and the wait for step j
+// leaves W(j+1) in flight.  `actual`: routed rows of the item (1..384).
+template <int NW>
+__device__ __forceinline__ void stage1_triple(const Stage1Params& p, const Work& w, int actual, char* smem) {
+  static_assert(NW == 8, "triple items run 8 waves");
+  constexpr int TR = 3 * kBN;        // token rows
+  constexpr int WR = kBN;            // weight rows: kBN / 2 gate, then kBN / 2 up
+  constexpr int TS = TR * kRowBytes;  // 48 KiB
+  constexpr int WS = WR * kRowBytes;  // 16 KiB
+  constexpr int NBM = 3;              // 32-row token blocks per wave
+  using LT = DmaTile<TR, NW>;
+  using LW = DmaTile<WR, NW>;
+  const int e = w.e, row0 = w.row0, n0 = w.n0;
+  const int64_t kbytes = p.H * 2;
+  const int nk = (int)(kbytes / kRowBytes);
+  const bool sh = p.e_shared >= 0 && e == p.e_shared;
+  const char* gexp = sh ? p.wg_shared : p.wg + (int64_t)e * p.w_es;
+  const char* uexp = sh ? p.wu_shared : p.wu + (int64_t)e * p.w_es;
+  LT ldt;
+  LW ldw;
+#pragma unroll
+  for (int i = 0; i < LT::NI; ++i) {
+    const int r = LT::row_of(i);
+    const int pid = r < actual ? p.sorted_ids[row0 + r] : 0;  // padding rows: token 0's row
+    ldt.set(i, p.x + (int64_t)(pid / p.topk) * kbytes);
+  }
+#pragma unroll
+  for (int i = 0; i < LW::NI; ++i) {
+    const int r = LW::row_of(i);
+    ldw.set(i, r < WR / 2 ? gexp + (int64_t)(n0 + r) * p.w_ld : uexp + (int64_t)(n0 + r - WR / 2) * p.w_ld);
+  }
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int xr0 = 32 * NBM * wm;      // stage row of this wave's first token row
+  const int gr0 = 32 * wn, ur0 = WR / 2 + 32 * wn;
+  const int live = (actual - xr0 + 31) / 32;  // this wave's blocks holding routed rows
+  const FragLane fl;
+  f32x16 ag[NBM], au[NBM];
+#pragma unroll
+  for (int b = 0; b < NBM; ++b) {
+    ag[b] = f32x16{};
+    au[b] = f32x16{};
+  }
+  auto tslot = [&](int j) { return smem + (j & 1) * TS; };
+  auto wslot = [&](int j) { return smem + 2 * TS + (j % 3) * WS; };
+  auto main_loop = [&](auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;
+    ldt.issue(tslot(0), 0);
+    ldw.issue(wslot(0), 0);
+    if (nk > 1) ldw.issue(wslot(1), 1);
+    for (int ks = 0; ks < nk; ++ks) {
+      // T(ks) and W(ks) are done when at most W(ks + 1)'s loads are outstanding
+      if (ks + 1 < nk) wait_vmcnt<LW::NI>();
+      else wait_vmcnt<0>();
+      barrier_no_fence();
+      if (ks + 1 < nk) ldt.issue(tslot(ks + 1), ks + 1);
+      if (ks + 2 < nk) ldw.issue(wslot(ks + 2), ks + 2);
+      if constexpr (NB > 0) {
+        u32x4 xf[2][NB], gf[2], uf[2];
+        const uint32_t xb = row_base(tslot(ks), xr0);
+        const uint32_t gb = row_base(wslot(ks), gr0), ub = row_base(wslot(ks), ur0);
+        auto load_frags = [&](int buf, int s) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) xf[buf][b] = frag_at(xb + 4096 * b, fl.off[s]);
+          gf[buf] = frag_at(gb, fl.off[s]);
+          uf[buf] = frag_at(ub, fl.off[s]);
+        };
+        load_frags(0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int fb = s & 1;
+          if (s < 3) load_frags(fb ^ 1, s + 1);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            ag[b] = mma(gf[fb], xf[fb][b], ag[b]);
+            au[b] = mma(uf[fb], xf[fb][b], au[b]);
+          }
+        }
+      }
+    }
+  };
+  with_live<NBM>(live < 0 ? 0 : live, main_loop);
+  // h = silu(g) * u -> fp16, routed rows only (as the other items' epilogue)
+  const int l = lane_id();
+#pragma unroll
+  for (int b = 0; b < NBM; ++b) {
+    const int m = xr0 + 32 * b + (l & 31);
+    if (m < actual) {
+      _Float16* hrow = reinterpret_cast<_Float16*>(p.h) + (int64_t)(row0 + m) * p.h_ld;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int n = n0 + 32 * wn + 8 * rg + 4 * (l >> 5);
+        f16x4 v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (_Float16)silu_mul(ag[b][4 * rg + q], au[b][4 * rg + q]);
+        *reinterpret_cast<f16x4*>(hrow + n) = v;
+      }
+    }
+  }
+}
+
 // One ring stage holds the tile's token rows, then its weight rows (Stage 1:
 // gate rows, then up rows), ROWS x 128 bytes in all, filled by one DmaTile;
 // fragment reads address it by stage row.
@@ -147,6 +267,9 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   static_assert(!PAIR || (BM == kBN && L::WAVES_N % 2 == 0), "a paired item must fill the same stage");
   static_assert(!(PAIR && F8), "fp8 quantises h per 128-column tile: items must span 128 columns");
   static_assert(S >= 2 && S * STAGE <= 160 * 1024, "LDS ring exceeds the 160 KiB of a CU");
+  constexpr bool TRI = MOE_S1_TRIPLE != 0 && ABS && PAIR && GATHER;  // triple items (stage1_triple)
+  static_assert(!TRI || (NW == 8 && 2 * 3 * kBN * kRowBytes + 3 * kBN * kRowBytes <= S * STAGE),
+                "a triple item's split ring must fit the stage ring's LDS");
   constexpr bool SPLIT = MOE_S1_SPLIT != 0 && I8 && !PAIR && BM == 2 * kBN && NW == 8;
   constexpr int HALF = (SPLIT ? BM : 0) * kRowBytes;  // one slot of the split ring: 32 KiB
   using LDH = DmaTile<SPLIT ? BM : 8 * NW, NW>;       // split ring: 256 rows per slot
@@ -157,7 +280,7 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   // gathered (fused) launches follow the align metadata; direct (pre-routed)
   // ones map block -> expert through gidx
   if (GATHER ? !schedule(blockIdx.x, p.gpo, p.E, BM, kBN, nt, p.host_blocks, false, PAIR, w, p.gs,
-                         ABS ? p.absorb : 0)
+                         ABS ? p.absorb : 0, TRI)
              : !schedule_bx(blockIdx.x, p.gidx, p.host_blocks, p.E, BM, kBN, nt, PAIR, w, p.gs, p.gpo,
                             ABS ? p.absorb : 0)) return;
   const int e = w.e;
@@ -170,6 +293,12 @@ __global__ __launch_bounds__(64 * NW) void stage1_kernel(Stage1Params p) {
   int actual = p.gs[e] - (row0 - gpo_e);
   actual = actual < 0 ? 0 : (actual > rx ? rx : actual);
   if (actual == 0) return;  // empty block: intermediate rows left untouched
+  if constexpr (TRI) {
+    if (w.rows == 3 * BM) {
+      stage1_triple<NW>(p, w, actual, smem);
+      return;
+    }
+  }
 
   const int64_t kbytes = p.H * (I8 ? 1 : 2);
   const int nk = (int)(kbytes / kRowBytes);

@@ -366,9 +366,9 @@ __device__ __forceinline__ uint32_t quant_code4(float x0, float x1, float x2, fl
 struct Work {
   int e;        // expert, or -1 for a tail block owned by no expert
   int row0;     // first row of the tile (in the expert-sorted row space)
-  int rows;     // BM, or 2*BM for a paired item
+  int rows;     // BM, 2*BM for a paired item, 3*BM for a triple item
   int n0;       // first output feature of the tile
-  int bn;       // BN, or BN/2 for a paired item
+  int bn;       // BN, or BN/2 for a paired or triple item
   bool shared;  // other items of this launch read the same weight rows
   int ar0 = 0;  // absorbed rows (see below): first sorted row ...
   int nar = 0;  // ... and count (0: none)
@@ -395,16 +395,29 @@ struct Work {
 constexpr int kAbsorbRows = 32;
 constexpr int kAbsorbMaxE = 256;
 
+// Triple items.  With pairing, an expert with an odd number nm >= 3 of blocks
+// holding items runs, per N tile, its (nm - 1) / 2 pairs on each half tile
+// and one single block over the whole tile; the single streams the tile
+// again at its own pace, and a 4 MiB L2 does not keep it across the lag.
+// With `triple` set (schedule_absorbed only), the expert's last three blocks
+// instead form one item per half tile, 3*BM rows x BN/2 features, so every
+// weight row of the expert's tile is streamed by exactly one item per pair
+// group: (nm - 1) * nt items instead of nm * nt.  An expert whose absorbed
+// rows would have to ride with the triple (nm == 3) keeps its pair and
+// single.
+
 
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
-                                                  int nt, int host_blocks, bool pair, int absorb, Work& w);
+                                                  int nt, int host_blocks, bool pair, int absorb, bool triple,
+                                                  Work& w);
 
 __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo, int E, int BM, int BN,
                                          int nt, int host_blocks, bool tail, bool pair, Work& w,
-                                         const int32_t* __restrict__ gs = nullptr, int absorb = 0) {
+                                         const int32_t* __restrict__ gs = nullptr, int absorb = 0,
+                                         bool triple = false) {
   if (absorb > 0 && !tail && E <= kAbsorbMaxE)
-    return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, absorb, w);
+    return schedule_absorbed(g, gpo, gs, E, BM, BN, nt, host_blocks, pair, absorb, triple, w);
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
   const int total_blocks = tail ? host_blocks : expert_blocks;
@@ -461,21 +474,24 @@ __device__ __forceinline__ bool schedule(int g, const int32_t* __restrict__ gpo,
 // schedule() with absorbed rows (E <= kAbsorbMaxE, no ownerless tail items).
 // Lane l scans expert 64c + l of chunk c: nb blocks, of which d (the last
 // block with routed rows, if absorbed, and any empty block after it) get no
-// items.  Expert e's items start at (gpo[e]/BM - sum of d below e) * nt,
-// counted with two ballots per chunk; the selected expert is the last whose
-// first item is <= the workgroup's item.
+// items, and one more block's worth of items goes when the expert takes a
+// triple item.  Expert e's items start at (gpo[e]/BM - sum of those below e)
+// * nt, counted with three ballots per chunk; the selected expert is the last
+// whose first item is <= the workgroup's item.
 __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restrict__ gpo,
                                                   const int32_t* __restrict__ gs, int E, int BM, int BN,
-                                                  int nt, int host_blocks, bool pair, int absorb, Work& w) {
+                                                  int nt, int host_blocks, bool pair, int absorb, bool triple,
+                                                  Work& w) {
   constexpr int C = kAbsorbMaxE / 64;
   const int l = lane_id();
   int cb0[C], cnb[C], cd[C];
-  uint64_t cm1[C], cm2[C];
+  uint64_t cm1[C], cm2[C], cm3[C];
   int dtot = 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int e = 64 * c + l;
     int b0 = 0, nb = 0, d = 0;
+    bool tri = false;
     if (e < E) {
       b0 = gpo[e] / BM;
       nb = gpo[e + 1] / BM - b0;
@@ -483,13 +499,16 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
       const int v = (n + BM - 1) / BM;  // blocks holding routed rows
       if (v >= (pair ? absorb : 1) + 1 && n - (v - 1) * BM <= kAbsorbRows && nb >= v && nb - (v - 1) <= 3)
         d = nb - (v - 1);
+      const int nm = nb - d;
+      tri = triple && pair && nm >= 3 && (nm & 1) && (d == 0 || nm >= 5);
     }
     cb0[c] = b0;
     cnb[c] = nb;
-    cd[c] = d;
+    cd[c] = d + (tri ? 4 : 0);  // bit 2: the expert takes a triple item
     cm1[c] = __ballot(d & 1);
     cm2[c] = __ballot((d >> 1) & 1);
-    dtot += __popcll(cm1[c]) + 2 * __popcll(cm2[c]);
+    cm3[c] = __ballot(tri);
+    dtot += __popcll(cm1[c]) + 2 * __popcll(cm2[c]) + __popcll(cm3[c]);
   }
   int expert_blocks = gpo[E] / BM;
   expert_blocks = expert_blocks < host_blocks ? expert_blocks : host_blocks;
@@ -502,7 +521,8 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
   int e = -1, eb0 = 0, enb = 0, ed = 0, estart = 0, carry = 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
-    const int start = (cb0[c] - carry - __popcll(cm1[c] & below) - 2 * __popcll(cm2[c] & below)) * nt;
+    const int start = (cb0[c] - carry - __popcll(cm1[c] & below) - 2 * __popcll(cm2[c] & below) -
+                       __popcll(cm3[c] & below)) * nt;
     const int k = __popcll(__ballot(64 * c + l < E && start <= v));
     if (k > 0) {  // wave-uniform
       e = 64 * c + k - 1;
@@ -511,22 +531,30 @@ __device__ __forceinline__ bool schedule_absorbed(int g, const int32_t* __restri
       ed = __shfl(cd[c], k - 1);
       estart = __shfl(start, k - 1);
     }
-    carry += __popcll(cm1[c]) + 2 * __popcll(cm2[c]);
+    carry += __popcll(cm1[c]) + 2 * __popcll(cm2[c]) + __popcll(cm3[c]);
   }
   if (e < 0) return false;  // only with inconsistent metadata (gpo[0] > 0)
+  const int etri = triple ? ed >> 2 : 0;  // the expert takes a triple item
+  if (triple) ed &= 3;
   const int nm = enb - ed;  // blocks with items
   if (nm <= 0) return false;
+  const int ni = nm - etri;  // items per N tile
   const int local = v - estart;
-  const int t = local / nm;  // N tile
-  const int r = local % nm;  // item within tile t
-  const int P = pair ? nm / 2 : 0;
+  const int t = local / ni;  // N tile
+  const int r = local % ni;  // item within tile t
+  const int P = pair ? (nm - 3 * etri) / 2 : 0;  // pairs per half tile (besides the triple)
   w.e = e;
-  w.shared = pair ? nm > 2 : nm > 1;
+  w.shared = pair ? ni > 2 : ni > 1;
   if (r < 2 * P) {
     w.rows = 2 * BM;
     w.row0 = (eb0 + 2 * (r % P)) * BM;
     w.bn = BN / 2;
     w.n0 = (2 * t + r / P) * (BN / 2);
+  } else if (etri) {  // r = 2P, 2P + 1: the triple on half tile r - 2P
+    w.rows = 3 * BM;
+    w.row0 = (eb0 + 2 * P) * BM;
+    w.bn = BN / 2;
+    w.n0 = (2 * t + r - 2 * P) * (BN / 2);
   } else {
     w.rows = BM;
     w.row0 = (eb0 + r) * BM;

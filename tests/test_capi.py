@@ -149,17 +149,23 @@ def test_256_row_padding_policy():
     assert ws(2048, 4224, 14336, 8, 2, 0, 0) == ws(2048, 4224, 14336, 8, 2, 128, 0)
 
 
-def test_scatter_reduce_variant_compiles(tmp_path):
-    """The Stage 2 scatter-reduce variant (MOE_S2_SCATTER=1: packed fp16
-    atomics into the token-ordered output, no combine) is kept as a committed
-    compile-time flag for its A/B; it must keep compiling for gfx950."""
+@pytest.mark.parametrize("define,sources", [
+    ("MOE_S2_SCATTER", ("grouped_gemm.hip", "capi.hip")),
+    ("MOE_S1_TRIPLE", ("grouped_gemm.hip",)),
+])
+def test_measured_variant_compiles(tmp_path, define, sources):
+    """Variants kept as committed compile-time flags for their A/B must keep
+    compiling for gfx950: the Stage 2 scatter-reduce (MOE_S2_SCATTER=1: packed
+    fp16 atomics into the token-ordered output, no combine) and Stage 1's
+    triple items (MOE_S1_TRIPLE=1: an odd multi-block expert's last three
+    blocks as one item per half weight tile)."""
     import subprocess
     from muxi_race_amd.build import CSRC, HIP_FLAGS, _hipcc
     try:
         hipcc = _hipcc()
     except RuntimeError:
         pytest.skip("hipcc not available")
-    for src in ("grouped_gemm.hip", "capi.hip"):
-        cmd = [hipcc, *HIP_FLAGS, "-DMOE_S2_SCATTER=1", "-c", str(CSRC / src), "-o", str(tmp_path / (src + ".o"))]
+    for src in sources:
+        cmd = [hipcc, *HIP_FLAGS, f"-D{define}=1", "-c", str(CSRC / src), "-o", str(tmp_path / (src + ".o"))]
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]

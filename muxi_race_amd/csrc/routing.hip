@@ -427,10 +427,12 @@ hipError_t launch_align(const int32_t* ids, int P, int E, int BM, int32_t* sorte
 // (an expert shard), only pairs routed to experts [e_lo, e_lo + e_n) are
 // summed: the others' rows were never written.
 // ---------------------------------------------------------------------------
+template <int KC>
 __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict__ y,
                                                       const int32_t* __restrict__ pos, int64_t T,
-                                                      int64_t H, int k, _Float16* __restrict__ out,
+                                                      int64_t H, int k_rt, _Float16* __restrict__ out,
                                                       const int32_t* __restrict__ ids, int e_lo, int e_n) {
+  const int k = KC > 0 ? KC : k_rt;  // KC > 0: k known at compile time (no masked batch slots)
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t cpr = H / 8;
   if (idx >= T * cpr) return;
@@ -438,22 +440,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const _Float16* __restrict
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const _Float16* src = y + 8 * c;
   const int32_t* prow = pos + t * k;
-  constexpr int kBatch = 8;
+  constexpr int kBatch = KC > 0 ? KC : 8;
   for (int j0 = 0; j0 < k; j0 += kBatch) {
-    f16x8 v[kBatch];
+    // Every load of the batch is issued unconditionally, positions first,
+    // then the pair rows: a predicated load compiles to a branch that waits
+    // for all earlier loads, which serialised a thread's k row loads.  A slot
+    // past k or a pair outside the expert range (whose position was never
+    // written) reads row 0 and is dropped by a select.
+    int32_t pj[kBatch];
     bool in[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      in[u] = j0 + u < k && (!ids || (unsigned)ids[t * k + j0 + u] - (unsigned)e_lo < (unsigned)e_n);
+    for (int u = 0; u < kBatch; ++u) {
+      const int j = j0 + u < k ? j0 + u : k - 1;  // an entry of token t (k >= 1)
+      pj[u] = prow[j];
+      in[u] = j0 + u < k && (!ids || (unsigned)ids[t * k + j] - (unsigned)e_lo < (unsigned)e_n);
+    }
+    f16x8 v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (in[u]) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)prow[j0 + u] * H));
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(src + (int64_t)(in[u] ? pj[u] : 0) * H));
+    __builtin_amdgcn_sched_barrier(0);  // every row load issued before any use
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
-      if (in[u]) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[q] += (float)v[u][q];
-      }
+      for (int q = 0; q < 8; ++q) acc[q] = in[u] ? acc[q] + (float)v[u][q] : acc[q];
   }
   f16x8 r;
 #pragma unroll
@@ -465,9 +475,15 @@ hipError_t launch_combine(const void* y_pair, const int32_t* pos, int64_t T, int
                           hipStream_t s, const int32_t* ids, int e_lo, int e_n) {
   const int64_t n = T * (H / 8);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                     reinterpret_cast<const _Float16*>(y_pair), pos, T, H, k,
-                     reinterpret_cast<_Float16*>(out), ids, e_lo, e_n);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  const _Float16* yp = reinterpret_cast<const _Float16*>(y_pair);
+  _Float16* o = reinterpret_cast<_Float16*>(out);
+  switch (k) {
+    case 2: hipLaunchKernelGGL(combine_kernel<2>, grid, block, 0, s, yp, pos, T, H, k, o, ids, e_lo, e_n); break;
+    case 6: hipLaunchKernelGGL(combine_kernel<6>, grid, block, 0, s, yp, pos, T, H, k, o, ids, e_lo, e_n); break;
+    case 8: hipLaunchKernelGGL(combine_kernel<8>, grid, block, 0, s, yp, pos, T, H, k, o, ids, e_lo, e_n); break;
+    default: hipLaunchKernelGGL(combine_kernel<0>, grid, block, 0, s, yp, pos, T, H, k, o, ids, e_lo, e_n); break;
+  }
   return hipGetLastError();
 }
 

@@ -575,18 +575,29 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # headline: K steps bracketed by synchronisation, per-step events for the median
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    # headline: K steps bracketed by synchronisation and two events, nothing
+    # recorded between the steps
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
+    t0.record()
+    for i in range(args.steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3
+    ms = t0.elapsed_time(t1) / args.steps
+
+    # per-step spread, a second pass with an event between steps: each record
+    # leaves a gap of a few microseconds between launches (small's step 25 ->
+    # 28.5 us with them), so this pass gives the median only, not the headline
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     evs[0].record()
     for i in range(args.steps):
         step()
         evs[i + 1].record()
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t_wall) * 1e3
     per = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
-    ms = evs[0].elapsed_time(evs[-1]) / args.steps
 
     # per-stage durations on the launch stream
     stage_names = ["route", "align", "quant_x", "stage1", "stage2", "combine"]

@@ -131,25 +131,35 @@ __device__ __forceinline__ void route_token_values(const float (&v)[VPL], uint32
   }
 }
 
-// Routes token t; logit(e) returns its logit for expert e (lane l asks for
-// experts l, l + 64, ...); kout as route_token_values (0: k).
-template <int VPL, typename Logit>
-__device__ __forceinline__ void route_token_with(Logit&& logit, const float* __restrict__ bias, int t, int E,
-                                                 int k, int32_t* __restrict__ ids, float* __restrict__ wout,
-                                                 int kout = 0, int e_shared = -1) {
+// Routes token t from its logits row (lane l takes experts l, l + 64, ...)
+// and the optional bias; kout as route_token_values (0: k).  Every value is
+// loaded unconditionally, at expert min(e, E - 1) (E >= 1), with the logits
+// row standing in for a missing bias, and selected afterwards: a load guarded
+// by e < E or by the bias compiles to a branch that waits for every earlier
+// load, one memory round trip per value instead of one for all.  The sum is
+// logit + bias only when a bias is given, as before (no + 0 that would turn a
+// -0 logit into +0).
+template <int VPL>
+__device__ __forceinline__ void route_token_row(const float* __restrict__ row, const float* __restrict__ bias,
+                                                int t, int E, int k, int32_t* __restrict__ ids,
+                                                float* __restrict__ wout, int kout = 0, int e_shared = -1) {
   const int l = lane_id();
+  const float* bsrc = bias ? bias : row;
+  float lv[VPL], bv[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = l + 64 * j;
+    const int ec = e < E ? e : E - 1;
+    lv[j] = row[ec];
+    bv[j] = bsrc[ec];
+  }
   float v[VPL];
   uint32_t valid = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int e = l + 64 * j;
-    v[j] = -INFINITY;
-    if (e < E) {
-      float x = logit(e);
-      if (bias) x = x + bias[e];
-      v[j] = x;
-      valid |= 1u << j;
-    }
+    const bool in = l + 64 * j < E;
+    v[j] = in ? (bias ? lv[j] + bv[j] : lv[j]) : -INFINITY;
+    valid |= in ? 1u << j : 0u;
   }
   route_token_values<VPL>(v, valid, t, k, ids, wout, kout == 0 ? k : kout, e_shared);
 }

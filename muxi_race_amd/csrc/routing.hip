@@ -18,9 +18,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
                                                          float* __restrict__ wout, int e_shared) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // uniform per wave
-  const float* row = logits + (int64_t)t * E;
-  route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout,
-                        e_shared >= 0 ? k + 1 : k, e_shared);
+  route_token_row<VPL>(logits + (int64_t)t * E, bias, t, E, k, ids, wout, e_shared >= 0 ? k + 1 : k, e_shared);
 }
 
 hipError_t launch_route_topk(const float* logits, const float* bias, int T, int E, int k,
@@ -608,29 +606,30 @@ __global__ __launch_bounds__(256) void route_quant_kernel(const float* __restric
   if constexpr (NCH > 0) {
     // logits (and bias) first, then the row: loads retire in order, so the
     // routing waits only for its own values while the row is in flight
+    // (unconditional loads at clamped experts, then selected: see route_token_row)
     const int l = lane_id();
+    const float* bsrc = bias ? bias : row;
     float lv[VPL], bv[VPL];
-    uint32_t valid = 0;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int e = l + 64 * j;
-      lv[j] = -INFINITY;
-      bv[j] = 0.0f;
-      if (e < E) {
-        lv[j] = row[e];
-        if (bias) bv[j] = bias[e];
-        valid |= 1u << j;
-      }
+      const int ec = e < E ? e : E - 1;
+      lv[j] = row[ec];
+      bv[j] = bsrc[ec];
     }
     f16x8 v[NCH];
     quant_row_load<NCH>(x + (int64_t)t * H, H, v);
+    uint32_t valid = 0;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (bias && (valid & (1u << j))) lv[j] = lv[j] + bv[j];
+    for (int j = 0; j < VPL; ++j) {
+      const bool in = l + 64 * j < E;
+      lv[j] = in ? (bias ? lv[j] + bv[j] : lv[j]) : -INFINITY;
+      valid |= in ? 1u << j : 0u;
+    }
     route_token_values<VPL>(lv, valid, t, k, ids, wout, k, -1);
     quant_row_store<NCH, F8>(v, H, xq + (int64_t)t * H, sx + t);
   } else {
-    route_token_with<VPL>([&](int e) { return row[e]; }, bias, t, E, k, ids, wout, k, -1);
+    route_token_row<VPL>(row, bias, t, E, k, ids, wout, k, -1);
     quant_row_wave<NCH, F8>(x + (int64_t)t * H, H, xq + (int64_t)t * H, sx + t);
   }
 }

@@ -9,7 +9,8 @@ of the logits must permute the output rows, the routing ids and the routing
 weights bit for bit, in every config and format.  A gather, padding,
 absorbed-row or combine mapping mistake breaks this at sizes the CPU oracle
 cannot check whole.  The same holds within one call: tokens that repeat other
-tokens must get their rows bit for bit."""
+tokens must get their rows bit for bit.  And for the reference operator
+(run_kernel), rows permuted inside each expert's group."""
 import pytest
 import torch
 
@@ -68,3 +69,35 @@ def test_identical_tokens_get_identical_rows(name, fmt):
     assert torch.isfinite(out).all()
     diff = (out[dst] != out[src]).any(dim=1)
     assert not diff.any(), f"{name} {fmt or 'fp16'}: {int(diff.sum())} of {dst.numel()} copies differ"
+
+
+@pytest.mark.parametrize("case", [1, 2, 3])
+def test_run_kernel_row_permutation_equivariance(case):
+    """The reference operator (run_kernel) on its published cases: permuting
+    the valid rows inside each expert's group, with their raw-order routing
+    weights, permutes the output rows bit for bit (padding rows stay 0)."""
+    from _cases import RB_CASES, prerouted_inputs, rb_group_sizes
+    from muxi_race_amd import run_kernel
+    cfg = RB_CASES[case]
+    sizes = rb_group_sizes(cfg)
+    x, wg, wu, wd, routed, gs, go, gpo, gidx = prerouted_inputs(sizes, cfg["hidden"], cfg["intermediate"],
+                                                                seed=305 + case)
+    P = x.shape[0]
+    g = torch.Generator().manual_seed(306 + case)
+    rp = torch.arange(P)                     # padded row -> source padded row
+    vp = torch.arange(routed.numel())        # raw index -> source raw index
+    for e, n in enumerate(sizes):
+        s = torch.randperm(n, generator=g)
+        p0, v0 = int(gpo[e]), int(go[e])
+        rp[p0:p0 + n] = p0 + s
+        vp[v0:v0 + n] = v0 + s
+    rp, vp = rp.cuda(), vp.cuda()
+    outs = []
+    for xx, rr in ((x, routed), (x[rp].contiguous(), routed[vp].contiguous())):
+        out = torch.full_like(x, float("nan"))
+        run_kernel(xx, wg, wu, wd, rr, gs, go, gpo, gidx, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0]).all()
+    diff = (outs[0][rp] != outs[1]).any(dim=1)
+    assert not diff.any(), f"case {case}: {int(diff.sum())} of {P} rows differ after permutation"

@@ -10,7 +10,8 @@ weights bit for bit, in every config and format.  A gather, padding,
 absorbed-row or combine mapping mistake breaks this at sizes the CPU oracle
 cannot check whole.  The same holds within one call: tokens that repeat other
 tokens must get their rows bit for bit.  And for the reference operator
-(run_kernel), rows permuted inside each expert's group."""
+(run_kernel), rows permuted inside each expert's group; and through the router
+GEMM, the shared expert and an expert-parallel shard."""
 import pytest
 import torch
 
@@ -101,3 +102,38 @@ def test_run_kernel_row_permutation_equivariance(case):
     assert torch.isfinite(outs[0]).all()
     diff = (outs[0][rp] != outs[1]).any(dim=1)
     assert not diff.any(), f"case {case}: {int(diff.sum())} of {P} rows differ after permutation"
+
+
+@pytest.mark.parametrize("name,mode", [("dsv3", "router"), ("decode", "router"), ("dsv3", "shared"),
+                                       ("mixtral", "shared"), ("dsv3", "shard")])
+def test_permutation_equivariance_other_entries(name, mode):
+    """The same token-permutation property through the router GEMM (logits
+    computed in the call from x and a router weight), with the always-on
+    shared expert, and for one expert-parallel shard (experts 32-63 of 256)."""
+    from muxi_race_amd import fused_moe
+    inp = moe_inputs(name, 307)
+    T, E, H, I = inp["T"], inp["E"], inp["H"], inp["I"]
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(308)).cuda()
+    g = torch.Generator(device="cuda").manual_seed(309)
+    w = (inp["wg"], inp["wu"], inp["wd"])
+    kw = dict(expert_bias=inp["bias"], return_routing=True)
+    if mode == "router":
+        kw["router_weight"] = (torch.randn((E, H), generator=g, device="cuda") / H ** 0.5).half()
+    elif mode == "shared":
+        kw["shared_expert"] = tuple(torch.randn(s, generator=g, device="cuda", dtype=torch.float16) * 0.02
+                                    for s in ((I, H), (I, H), (H, I)))
+    else:
+        b, n = 32, 32
+        w = tuple(t[b:b + n] for t in w)
+        kw["expert_range"] = (b, n)
+
+    def run(x, lg):
+        return fused_moe(x, None if mode == "router" else lg, *w, inp["k"], **kw)
+
+    out, (ids, wts) = run(inp["x"], inp["logits"])
+    outp, (idsp, wtsp) = run(inp["x"][perm].contiguous(), inp["logits"][perm].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(ids[perm], idsp) and torch.equal(wts[perm], wtsp), "routing not per-token"
+    assert torch.isfinite(out).all()
+    diff = (out[perm] != outp).any(dim=1)
+    assert not diff.any(), f"{name} {mode}: {int(diff.sum())} of {T} rows differ after permutation"
